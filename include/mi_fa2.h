@@ -1,0 +1,129 @@
+/*
+ * mi_fa2.h -- C ABI of the MI355X (gfx950) FlashAttention-2 forward library, libmi_fa2.so.
+ *
+ * The library replaces the attention hot path of shubhav1/my-inference-engine:
+ *   - the Triton kernel `fa2_forward`            (kernels/fa2.py:14-162),
+ *   - its launcher `FlashAttention2Function`     (kernels/fa2.py:164-214),
+ *   - the per-step dense K/V gather it is fed by (kv_cache.py:117-121, called at model.py:97),
+ * with hand-written HIP kernels: an MFMA/LDS-tiled prefill kernel, a split-KV decode kernel that
+ * reads K/V straight out of the paged cache's blocks, and a split combine kernel.
+ *
+ * Conventions shared by every entry point
+ *   - All pointers are device pointers except the stride arrays, which are host arrays.
+ *   - Strides are in ELEMENTS, int64.  The innermost (head_dim) stride must be 1, every other stride
+ *     a multiple of 8 elements and every tensor base 16-byte aligned (16-byte vector loads).
+ *   - `dtype` is MI_FA2_BF16 or MI_FA2_FP16; q, k, v and o share it.  Softmax and accumulation
+ *     are fp32; `lse` is fp32 (natural log, like the reference's L, kernels/fa2.py:158,189).
+ *   - head_dim must be 128 (the Qwen2.5 shape); heads_q must be a multiple of heads_kv and query
+ *     head h reads kv head h / (heads_q / heads_kv) (kernels/fa2.py:53, model.py:70-75).
+ *   - Causal masking is bottom-right aligned per row: query i of a row sees key j iff
+ *     j <= i + kv_len - seqlen_q (kernels/fa2.py:109-111,132-138).  Keys j >= kv_len are never read
+ *     as data: their loads are predicated off, so padding may hold anything, NaN included.
+ *   - A query that sees no key gets an output of 0 and an lse of -inf.  This matches the
+ *     reference's fp32 SDPA path (model.py:104-107, kernels/test_fa2.py:28-35); the reference's
+ *     Triton kernel would produce 0/0 = NaN there.
+ *   - Launches are asynchronous on `stream` (a hipStream_t); nothing is synchronised and nothing
+ *     is allocated.  Entry points that need scratch take a caller-owned workspace whose size the
+ *     matching *_workspace_size() returns.
+ *   - Return value: MI_FA2_OK (0) or an error code; mi_fa2_last_error() then describes it.
+ */
+#ifndef MI_FA2_H
+#define MI_FA2_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI_FA2_API __attribute__((visibility("default")))
+
+typedef struct ihipStream_t* mi_fa2_stream_t; /* the same handle type as hipStream_t */
+
+enum mi_fa2_status {
+  MI_FA2_OK = 0,
+  MI_FA2_ERR_INVALID = 1,     /* bad pointer, shape, stride or alignment */
+  MI_FA2_ERR_UNSUPPORTED = 2, /* valid request outside the kernels' envelope (e.g. head_dim 64) */
+  MI_FA2_ERR_WORKSPACE = 3,   /* workspace missing or smaller than *_workspace_size() */
+  MI_FA2_ERR_LAUNCH = 4       /* the HIP runtime refused the launch */
+};
+
+enum mi_fa2_dtype { MI_FA2_BF16 = 0, MI_FA2_FP16 = 1 };
+
+/* Library version string, e.g. "mi_fa2 0.1.0 gfx950". */
+MI_FA2_API const char* mi_fa2_version(void);
+
+/* Message describing the most recent failing call on this thread ("" if none). */
+MI_FA2_API const char* mi_fa2_last_error(void);
+
+/*
+ * Padded forward.  Replaces FlashAttention2Function.forward (kernels/fa2.py:164-214) and the Triton
+ * launch at kernels/fa2.py:192-207, same argument meaning:
+ *   q [batch, heads_q, seqlen_q, 128], k/v [batch, heads_kv, seqlen_k, 128], o like q,
+ *   lse [batch, heads_q, seqlen_q] fp32 (may be NULL), kv_lens [batch] int32 (may be NULL: every
+ *   row uses all seqlen_k keys, kernels/fa2.py:182-183; values are clamped to [0, seqlen_k]).
+ *   q_strides/k_strides/v_strides/o_strides: 4 strides each; lse_strides: 3 (ignored if lse NULL).
+ * seqlen_q == 1 runs the split-KV decode kernel, which needs the workspace; seqlen_q > 1 runs the
+ * MFMA prefill kernel, which needs none.
+ */
+MI_FA2_API size_t mi_fa2_fwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv,
+                                 int32_t seqlen_q, int32_t seqlen_k, int32_t head_dim);
+MI_FA2_API int mi_fa2_fwd(int32_t dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+               const int32_t* kv_lens, int32_t batch, int32_t heads_q, int32_t heads_kv,
+               int32_t seqlen_q, int32_t seqlen_k, int32_t head_dim,
+               const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+               const int64_t* o_strides, const int64_t* lse_strides, int32_t is_causal,
+               float sm_scale, void* workspace, size_t workspace_bytes, mi_fa2_stream_t stream);
+
+/*
+ * Packed variable-length forward.  The reference has no packed entry point: it pads a ragged
+ * batch to the longest row and masks each row to its kv_lens (kv_cache.py:93-98,
+ * kernels/fa2.py:107,133).  This entry point computes the same per-row attention without the
+ * padding: row b owns query tokens [cu_seqlens_q[b], cu_seqlens_q[b+1]) of
+ *   q [total_q, heads_q, 128] and key tokens [cu_seqlens_k[b], cu_seqlens_k[b+1]) of
+ *   k/v [total_k, heads_kv, 128]; o like q; lse [heads_q, total_q] fp32 (may be NULL).
+ *   *_strides: 2 strides each (token, head); lse_strides: 2 (head, token).
+ * max_seqlen_q bounds every row's query count (it sizes the grid).
+ */
+MI_FA2_API int mi_fa2_fwd_varlen(int32_t dtype, const void* q, const void* k, const void* v, void* o,
+                      float* lse, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                      int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t max_seqlen_q,
+                      int32_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
+                      const int64_t* v_strides, const int64_t* o_strides,
+                      const int64_t* lse_strides, int32_t is_causal, float sm_scale,
+                      mi_fa2_stream_t stream);
+
+/*
+ * Paged forward: attention whose K/V are read in-kernel from the paged KV cache.  Replaces
+ * KVCache.read (kv_cache.py:117-121) + FlashAttention2Function.apply (model.py:97,103).
+ *   k_pool/v_pool: one layer of KVCache.buf, i.e. buf[layer, 0] and buf[layer, 1], each
+ *     [num_blocks * block_size, heads_kv, 128] (kv_cache.py:20-22); pool_strides: (slot, head)
+ *     strides, shared by k_pool and v_pool.
+ *   block_table [batch, >= ceil(kv_len/block_size)] int32, row stride block_table_stride:
+ *     logical token p of row b lives in slot block_table[b][p / block_size] * block_size +
+ *     p % block_size (kv_cache.py:15-16).  Entries past a row's kv_len are never read.  An entry
+ *     outside [0, num_blocks) is a caller bug; as a guard it is never dereferenced and its keys
+ *     read as zero vectors.
+ *   kv_lens [batch] int32: keys held by each row, this step's included (model.py:175).
+ *   max_kv_len: an upper bound of kv_lens (sizes the grid and the workspace).
+ *   q/o [batch, heads_q, seqlen_q, 128] with 4 strides; lse [batch, heads_q, seqlen_q] (may be NULL).
+ * block_size must be a multiple of 16.  seqlen_q == 1 is the decode regime (split-KV, uses the
+ * workspace); seqlen_q > 1 is a prefill over cached context (bottom-right causal if is_causal).
+ */
+MI_FA2_API size_t mi_fa2_fwd_paged_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv,
+                                       int32_t seqlen_q, int32_t max_kv_len, int32_t head_dim);
+MI_FA2_API int mi_fa2_fwd_paged(int32_t dtype, const void* q, const void* k_pool, const void* v_pool,
+                     void* o, float* lse, const int32_t* block_table, int64_t block_table_stride,
+                     const int32_t* kv_lens, int32_t batch, int32_t heads_q, int32_t heads_kv,
+                     int32_t seqlen_q, int32_t max_kv_len, int32_t head_dim, int32_t block_size,
+                     int32_t num_blocks, const int64_t* q_strides, const int64_t* pool_strides,
+                     const int64_t* o_strides, const int64_t* lse_strides, int32_t is_causal,
+                     float sm_scale, void* workspace, size_t workspace_bytes,
+                     mi_fa2_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI_FA2_H */

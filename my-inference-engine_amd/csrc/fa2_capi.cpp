@@ -1,0 +1,292 @@
+// C ABI of libmi_fa2.so: argument validation, split-KV sizing and kernel dispatch.
+// Declarations and the contract of every entry point are in include/mi_fa2.h.
+#include "mi_fa2.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "fa2_common.h"
+
+namespace mi_fa2 {
+hipError_t launch_prefill(const FwdParams& p, int dtype, int mode, int max_seqlen_q,
+                          hipStream_t stream);
+hipError_t launch_decode(const FwdParams& p, int dtype, int mode, hipStream_t stream);
+}  // namespace mi_fa2
+
+using mi_fa2::FwdParams;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return MI_FA2_OK;
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+// Keys per split of the decode kernel: 4 waves x 32 keys at least, doubled until the grid holds at
+// most ~4096 work-groups (about 16 per CU on 256 CUs), so long rows get enough parallelism while a
+// split stays long enough to amortise its set-up and partial write.
+int decode_chunk(int64_t batch, int64_t heads_kv, int64_t max_kv) {
+  int chunk = 128;
+  while (chunk < (1 << 16) && batch * heads_kv * ((max_kv + chunk - 1) / chunk) > 4096) chunk *= 2;
+  return chunk;
+}
+
+int decode_splits(int64_t max_kv, int chunk) {
+  return max_kv > 0 ? (int)((max_kv + chunk - 1) / chunk) : 1;
+}
+
+size_t decode_workspace(int64_t batch, int64_t heads_q, int64_t heads_kv, int64_t max_kv) {
+  const int chunk = decode_chunk(batch, heads_kv, max_kv);
+  const int splits = decode_splits(max_kv, chunk);
+  if (splits <= 1) return 0;
+  return (size_t)batch * heads_q * splits * (mi_fa2::kHeadDim + 2) * sizeof(float);
+}
+
+int check_common(int32_t dtype, int32_t batch, int32_t heads_q, int32_t heads_kv,
+                 int32_t head_dim) {
+  if (dtype != MI_FA2_BF16 && dtype != MI_FA2_FP16)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "dtype %d is not bf16 (0) or fp16 (1)", dtype);
+  if (batch < 0 || heads_q <= 0 || heads_kv <= 0)
+    return fail(MI_FA2_ERR_INVALID, "bad sizes: batch=%d heads_q=%d heads_kv=%d", batch, heads_q,
+                heads_kv);
+  if (heads_q % heads_kv != 0)
+    return fail(MI_FA2_ERR_INVALID, "heads_q (%d) must be a multiple of heads_kv (%d)", heads_q,
+                heads_kv);
+  if (head_dim != mi_fa2::kHeadDim)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "head_dim %d: the kernels are built for head_dim 128",
+                head_dim);
+  return MI_FA2_OK;
+}
+
+int check_tensor(const char* name, const void* ptr, const int64_t* strides, int n_outer) {
+  if (!ptr) return fail(MI_FA2_ERR_INVALID, "%s is NULL", name);
+  if (!aligned16(ptr)) return fail(MI_FA2_ERR_INVALID, "%s is not 16-byte aligned", name);
+  if (!strides) return fail(MI_FA2_ERR_INVALID, "%s strides are NULL", name);
+  for (int i = 0; i < n_outer; ++i)
+    if (strides[i] % 8 != 0)
+      return fail(MI_FA2_ERR_INVALID, "%s stride[%d] = %lld is not a multiple of 8 elements", name,
+                  i, (long long)strides[i]);
+  return MI_FA2_OK;
+}
+
+int launched(hipError_t err) {
+  if (err != hipSuccess)
+    return fail(MI_FA2_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return ok();
+}
+
+void set_lse(FwdParams& p, float* lse, const int64_t* s, int n) {
+  p.lse = lse;
+  if (!lse) return;
+  if (n == 3) {
+    p.l_sb = s[0];
+    p.l_sh = s[1];
+    p.l_st = s[2];
+  } else {  // varlen: (head, token)
+    p.l_sh = s[0];
+    p.l_st = s[1];
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mi_fa2_version(void) { return "mi_fa2 0.1.0 gfx950"; }
+
+const char* mi_fa2_last_error(void) { return g_err; }
+
+size_t mi_fa2_fwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv,
+                                 int32_t seqlen_q, int32_t seqlen_k, int32_t head_dim) {
+  (void)head_dim;
+  if (seqlen_q != 1 || heads_kv <= 0 || heads_q % heads_kv || heads_q / heads_kv > 16) return 0;
+  return decode_workspace(batch, heads_q, heads_kv, seqlen_k);
+}
+
+int mi_fa2_fwd(int32_t dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+               const int32_t* kv_lens, int32_t batch, int32_t heads_q, int32_t heads_kv,
+               int32_t seqlen_q, int32_t seqlen_k, int32_t head_dim, const int64_t* q_strides,
+               const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+               const int64_t* lse_strides, int32_t is_causal, float sm_scale, void* workspace,
+               size_t workspace_bytes, mi_fa2_stream_t stream) {
+  if (int rc = check_common(dtype, batch, heads_q, heads_kv, head_dim)) return rc;
+  if (seqlen_q < 0 || seqlen_k < 0)
+    return fail(MI_FA2_ERR_INVALID, "bad lengths: seqlen_q=%d seqlen_k=%d", seqlen_q, seqlen_k);
+  if (batch == 0 || seqlen_q == 0) return ok();
+  if (int rc = check_tensor("q", q, q_strides, 3)) return rc;
+  if (int rc = check_tensor("o", o, o_strides, 3)) return rc;
+  if (seqlen_k > 0) {
+    if (int rc = check_tensor("k", k, k_strides, 3)) return rc;
+    if (int rc = check_tensor("v", v, v_strides, 3)) return rc;
+  }
+  if (lse && !lse_strides) return fail(MI_FA2_ERR_INVALID, "lse strides are NULL");
+
+  FwdParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.o = static_cast<uint16_t*>(o);
+  p.kv_lens = kv_lens;
+  p.q_sb = q_strides[0], p.q_sh = q_strides[1], p.q_st = q_strides[2];
+  p.o_sb = o_strides[0], p.o_sh = o_strides[1], p.o_st = o_strides[2];
+  if (seqlen_k > 0) {
+    p.k_sb = k_strides[0], p.k_sh = k_strides[1], p.k_st = k_strides[2];
+    p.v_sb = v_strides[0], p.v_sh = v_strides[1], p.v_st = v_strides[2];
+  }
+  set_lse(p, lse, lse_strides, 3);
+  p.B = batch;
+  p.Hq = heads_q;
+  p.Hkv = heads_kv;
+  p.group = heads_q / heads_kv;
+  p.T = seqlen_q;
+  p.S = seqlen_k;
+  p.causal = is_causal ? 1 : 0;
+  p.scale_log2 = sm_scale * mi_fa2::kLog2e;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+
+  if (seqlen_q == 1 && p.group <= 16) {
+    p.chunk = decode_chunk(batch, heads_kv, seqlen_k);
+    p.max_splits = decode_splits(seqlen_k, p.chunk);
+    const size_t need = decode_workspace(batch, heads_q, heads_kv, seqlen_k);
+    if (need) {
+      if (!workspace || workspace_bytes < need)
+        return fail(MI_FA2_ERR_WORKSPACE, "decode needs %zu workspace bytes, got %zu", need,
+                    workspace ? workspace_bytes : (size_t)0);
+      float* ws = static_cast<float*>(workspace);
+      const size_t slots = (size_t)batch * heads_q * p.max_splits;
+      p.ws_o = ws;
+      p.ws_m = ws + slots * mi_fa2::kHeadDim;
+      p.ws_l = p.ws_m + slots;
+    }
+    return launched(mi_fa2::launch_decode(p, dtype, mi_fa2::kDense, s));
+  }
+  return launched(mi_fa2::launch_prefill(p, dtype, mi_fa2::kDense, seqlen_q, s));
+}
+
+int mi_fa2_fwd_varlen(int32_t dtype, const void* q, const void* k, const void* v, void* o,
+                      float* lse, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                      int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t max_seqlen_q,
+                      int32_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
+                      const int64_t* v_strides, const int64_t* o_strides,
+                      const int64_t* lse_strides, int32_t is_causal, float sm_scale,
+                      mi_fa2_stream_t stream) {
+  if (int rc = check_common(dtype, batch, heads_q, heads_kv, head_dim)) return rc;
+  if (max_seqlen_q < 0) return fail(MI_FA2_ERR_INVALID, "max_seqlen_q %d < 0", max_seqlen_q);
+  if (batch == 0 || max_seqlen_q == 0) return ok();
+  if (!cu_seqlens_q || !cu_seqlens_k) return fail(MI_FA2_ERR_INVALID, "cu_seqlens are NULL");
+  if (int rc = check_tensor("q", q, q_strides, 2)) return rc;
+  if (int rc = check_tensor("k", k, k_strides, 2)) return rc;
+  if (int rc = check_tensor("v", v, v_strides, 2)) return rc;
+  if (int rc = check_tensor("o", o, o_strides, 2)) return rc;
+  if (lse && !lse_strides) return fail(MI_FA2_ERR_INVALID, "lse strides are NULL");
+
+  FwdParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.o = static_cast<uint16_t*>(o);
+  p.cu_q = cu_seqlens_q;
+  p.cu_k = cu_seqlens_k;
+  p.q_st = q_strides[0], p.q_sh = q_strides[1];
+  p.k_st = k_strides[0], p.k_sh = k_strides[1];
+  p.v_st = v_strides[0], p.v_sh = v_strides[1];
+  p.o_st = o_strides[0], p.o_sh = o_strides[1];
+  set_lse(p, lse, lse_strides, 2);
+  p.B = batch;
+  p.Hq = heads_q;
+  p.Hkv = heads_kv;
+  p.group = heads_q / heads_kv;
+  p.causal = is_causal ? 1 : 0;
+  p.scale_log2 = sm_scale * mi_fa2::kLog2e;
+  return launched(mi_fa2::launch_prefill(p, dtype, mi_fa2::kVarlen, max_seqlen_q,
+                                         reinterpret_cast<hipStream_t>(stream)));
+}
+
+size_t mi_fa2_fwd_paged_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv,
+                                       int32_t seqlen_q, int32_t max_kv_len, int32_t head_dim) {
+  return mi_fa2_fwd_workspace_size(batch, heads_q, heads_kv, seqlen_q, max_kv_len, head_dim);
+}
+
+int mi_fa2_fwd_paged(int32_t dtype, const void* q, const void* k_pool, const void* v_pool,
+                     void* o, float* lse, const int32_t* block_table, int64_t block_table_stride,
+                     const int32_t* kv_lens, int32_t batch, int32_t heads_q, int32_t heads_kv,
+                     int32_t seqlen_q, int32_t max_kv_len, int32_t head_dim, int32_t block_size,
+                     int32_t num_blocks, const int64_t* q_strides, const int64_t* pool_strides,
+                     const int64_t* o_strides, const int64_t* lse_strides, int32_t is_causal,
+                     float sm_scale, void* workspace, size_t workspace_bytes,
+                     mi_fa2_stream_t stream) {
+  if (int rc = check_common(dtype, batch, heads_q, heads_kv, head_dim)) return rc;
+  if (seqlen_q < 0 || max_kv_len < 0)
+    return fail(MI_FA2_ERR_INVALID, "bad lengths: seqlen_q=%d max_kv_len=%d", seqlen_q,
+                max_kv_len);
+  if (block_size < 16 || (block_size & (block_size - 1)))
+    return fail(MI_FA2_ERR_UNSUPPORTED, "block_size %d is not a power of two >= 16", block_size);
+  if (num_blocks < 0) return fail(MI_FA2_ERR_INVALID, "num_blocks %d < 0", num_blocks);
+  if (batch == 0 || seqlen_q == 0) return ok();
+  if (!kv_lens) return fail(MI_FA2_ERR_INVALID, "kv_lens is NULL");
+  if (max_kv_len > 0 && !block_table) return fail(MI_FA2_ERR_INVALID, "block_table is NULL");
+  if (int rc = check_tensor("q", q, q_strides, 3)) return rc;
+  if (int rc = check_tensor("o", o, o_strides, 3)) return rc;
+  if (int rc = check_tensor("k_pool", k_pool, pool_strides, 2)) return rc;
+  if (int rc = check_tensor("v_pool", v_pool, pool_strides, 2)) return rc;
+  if (lse && !lse_strides) return fail(MI_FA2_ERR_INVALID, "lse strides are NULL");
+
+  FwdParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k_pool);
+  p.v = static_cast<const uint16_t*>(v_pool);
+  p.o = static_cast<uint16_t*>(o);
+  p.kv_lens = kv_lens;
+  p.block_table = block_table;
+  p.bt_stride = block_table_stride;
+  p.block_size = block_size;
+  p.num_blocks = num_blocks;
+  p.q_sb = q_strides[0], p.q_sh = q_strides[1], p.q_st = q_strides[2];
+  p.o_sb = o_strides[0], p.o_sh = o_strides[1], p.o_st = o_strides[2];
+  p.k_st = pool_strides[0], p.k_sh = pool_strides[1];
+  p.v_st = pool_strides[0], p.v_sh = pool_strides[1];
+  set_lse(p, lse, lse_strides, 3);
+  p.B = batch;
+  p.Hq = heads_q;
+  p.Hkv = heads_kv;
+  p.group = heads_q / heads_kv;
+  p.T = seqlen_q;
+  p.S = max_kv_len;
+  p.causal = is_causal ? 1 : 0;
+  p.scale_log2 = sm_scale * mi_fa2::kLog2e;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+
+  if (seqlen_q == 1 && p.group <= 16) {
+    p.chunk = decode_chunk(batch, heads_kv, max_kv_len);
+    p.max_splits = decode_splits(max_kv_len, p.chunk);
+    const size_t need = decode_workspace(batch, heads_q, heads_kv, max_kv_len);
+    if (need) {
+      if (!workspace || workspace_bytes < need)
+        return fail(MI_FA2_ERR_WORKSPACE, "decode needs %zu workspace bytes, got %zu", need,
+                    workspace ? workspace_bytes : (size_t)0);
+      float* ws = static_cast<float*>(workspace);
+      const size_t slots = (size_t)batch * heads_q * p.max_splits;
+      p.ws_o = ws;
+      p.ws_m = ws + slots * mi_fa2::kHeadDim;
+      p.ws_l = p.ws_m + slots;
+    }
+    return launched(mi_fa2::launch_decode(p, dtype, mi_fa2::kPaged, s));
+  }
+  return launched(mi_fa2::launch_prefill(p, dtype, mi_fa2::kPaged, seqlen_q, s));
+}
+
+}  // extern "C"

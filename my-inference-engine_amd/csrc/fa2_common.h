@@ -1,0 +1,112 @@
+// Shared device-side definitions of the gfx950 attention kernels: vector types, the MFMA wrappers
+// for bf16/fp16, fp32 -> 16-bit packing, and the parameter block every kernel receives.
+//
+// MFMA operand layouts used throughout (wave64, gfx950):
+//   v_mfma_f32_32x32x16_{bf16,f16}: A[m][k] lane l holds row m = l%32 and 8 k-values; B[k][n] lane l
+//     holds column n = l%32 and the same 8 k-slots; D[m][n] lane l holds column n = l%32 and rows
+//     m = 8*(r/4) + 4*(l/32) + r%4 for its 16 accumulators r.
+//   v_mfma_f32_16x16x32_{bf16,f16}: A lane l holds row m = l%16, B column n = l%16, 8 k-slots each;
+//     D lane l holds column n = l%16 and rows m = 4*(l/16) + r for its 4 accumulators r.
+// The kernels only rely on A and B sharing the k-slot order (any permutation of the contraction
+// index inside one MFMA gives the same sum), so they choose the k <-> slot mapping that makes
+// every operand a plain 16- or 8-byte load.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mi_fa2 {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kHeadDim = 128;
+constexpr float kLn2 = 0.69314718055994530942f;
+constexpr float kLog2e = 1.44269504088896340736f;
+
+// KV addressing modes.
+//   kDense : row b, head h, token t at base + b*s_b + h*s_h + t*s_t (the padded [B,H,S,d] layout)
+//   kVarlen: token t of row b at base + (cu_k[b] + t)*s_t + h*s_h (packed [total, H, d])
+//   kPaged : token t of row b at base + (table[b][t/bs]*bs + t%bs)*s_t + h*s_h (KVCache pool)
+enum KvMode { kDense = 0, kVarlen = 1, kPaged = 2 };
+
+struct BF16 {
+  static __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  // Round-to-nearest-even fp32 -> bf16 of two values, low half = lo.
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    bf16x2 v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+struct FP16 {
+  static __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    f16x2 v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+// Everything a kernel launch needs; passed by value (kernel argument segment).
+struct FwdParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  float* lse;                 // may be null
+  const int32_t* kv_lens;     // kDense/kPaged: [B] keys per row; null = all S (kDense only)
+  const int32_t* cu_q;        // kVarlen: [B+1] query offsets
+  const int32_t* cu_k;        // kVarlen: [B+1] key offsets
+  const int32_t* block_table; // kPaged: [B][bt_stride]
+  int64_t bt_stride;
+  int32_t block_size;         // kPaged: tokens per block, multiple of 16
+  int32_t num_blocks;         // kPaged: blocks in the pool
+  // element strides; for kVarlen the *_sb strides are unused and *_st is the packed token stride
+  int64_t q_sb, q_sh, q_st;
+  int64_t k_sb, k_sh, k_st;
+  int64_t v_sb, v_sh, v_st;
+  int64_t o_sb, o_sh, o_st;
+  int64_t l_sb, l_sh, l_st;
+  int32_t B, Hq, Hkv, group;  // group = Hq / Hkv
+  int32_t T;                  // query rows per batch row (padded modes)
+  int32_t S;                  // key capacity per row (upper bound of kv_lens)
+  int32_t causal;
+  float scale_log2;           // sm_scale * log2(e): scores are kept in the exp2 domain
+  // split-KV decode workspace (fp32): partial O [B][Hq][max_splits][128], m and l [B][Hq][max_splits]
+  float* ws_o;
+  float* ws_m;
+  float* ws_l;
+  int32_t chunk;              // keys per split
+  int32_t max_splits;
+};
+
+__device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+__device__ __forceinline__ float fmax3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Keys held by row b, clamped to [0, cap].
+__device__ __forceinline__ int clamp_len(int n, int cap) { return n < 0 ? 0 : (n > cap ? cap : n); }
+
+}  // namespace mi_fa2

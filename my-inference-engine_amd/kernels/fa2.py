@@ -1,0 +1,198 @@
+"""FlashAttention-2 forward on MI355X: drop-in for the reference's kernels/fa2.py.
+
+`FlashAttention2Function.apply(Q, K, V, is_causal=False, kv_lens=None) -> O` keeps the call
+signature, argument meaning, checks (AssertionError) and outputs of kernels/fa2.py:164-214, so the
+reference's model.py:11-15,102-103 import and call it unchanged.  The Triton launch
+(kernels/fa2.py:192-207) is replaced by one call into libmi_fa2.so's C ABI, which runs hand-written
+gfx950 kernels on torch's current stream:
+
+  * seqlen_q > 1: the MFMA prefill kernel (csrc/fa2_prefill.hip);
+  * seqlen_q == 1: the split-KV decode kernel + combine (csrc/fa2_decode.hip).
+
+Two entry points go beyond the reference's padded call:
+
+  * `fa2_paged(q, k_pool, v_pool, block_table, kv_lens, ...)` reads K/V straight out of a
+    KVCache-layout pool (kv_cache.py:20-22) through a block table, replacing
+    KVCache.read's per-step dense gather (kv_cache.py:117-121) + the padded call.
+  * `fa2_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, is_causal)` runs a ragged
+    batch packed back to back (no padding).
+
+The HIP kernels cover head_dim 128 in bf16/fp16 (the Qwen2.5-1.5B shape the engine runs).
+Anything else is rejected with an AssertionError, never silently computed another way.
+"""
+import math
+
+import torch
+
+from . import _lib
+
+HEAD_DIM = 128
+
+
+def _dims_ok(t):
+    return t.data_ptr() % 16 == 0 and t.stride(-1) == 1 and all(
+        st % 8 == 0 for st, n in zip(t.stride()[:-1], t.shape[:-1]) if n > 1)
+
+
+def _vec(t):
+    """t, or a contiguous copy if its layout does not allow 16-byte vector loads."""
+    return t if _dims_ok(t) else t.contiguous()
+
+
+def _strides(t):
+    # a size-1 dimension is only ever indexed at 0, so its stride is irrelevant: pass 0
+    s = [0 if n == 1 else st for st, n in zip(t.stride(), t.shape)]
+    return (_lib.ctypes.c_int64 * len(s))(*s)
+
+
+def _envelope(Q, K, V):
+    assert Q.dtype in _lib.DTYPES, f"the MI355X kernels take bf16 or fp16 inputs, got {Q.dtype}"
+    assert K.dtype == Q.dtype and V.dtype == Q.dtype, "Q, K and V must share one dtype"
+    assert Q.shape[-1] == HEAD_DIM and V.shape[-1] == HEAD_DIM, (
+        f"the MI355X kernels are built for head_dim {HEAD_DIM}, got d={Q.shape[-1]}, d_v={V.shape[-1]}")
+    assert K.device == Q.device and V.device == Q.device, "Q, K and V must be on one device"
+
+
+def _workspace(nbytes, device):
+    return torch.empty(max(int(nbytes), 0), dtype=torch.uint8, device=device) if nbytes else None
+
+
+class FlashAttention2Function(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, Q, K, V, is_causal=False, kv_lens=None):
+        # Q [B, Hq, T, d], K/V [B, Hkv, S, d]; kv_lens [B] int32: real keys per row (the rest of
+        # K/V is padding); causal masking is aligned to each row's last key.
+        batch_size, num_heads, seq_len, d = Q.shape
+        seq_len_k = K.shape[2]
+        d_v = V.shape[-1]
+        sm_scale = 1.0 / math.sqrt(d)
+
+        assert Q.is_cuda and K.is_cuda and V.is_cuda, "Q, K and V must be GPU tensors"
+        num_kv_heads = K.shape[1]
+        assert Q.shape[0] == K.shape[0] and Q.shape[-1] == K.shape[-1], \
+            "Q and K must agree in batch size and head dim"
+        assert num_heads % num_kv_heads == 0, "query heads must be a multiple of kv heads (GQA)"
+        assert K.shape[:-1] == V.shape[:-1], "K and V may differ only in their last dimension"
+        if kv_lens is not None:
+            assert kv_lens.shape == (batch_size,) and kv_lens.dtype == torch.int32, \
+                "kv_lens must be an int32 tensor of shape [batch]"
+            assert kv_lens.device == Q.device, "kv_lens must be on Q's device"
+        assert (d & (d - 1) == 0) and (d_v & (d_v - 1) == 0), "d and d_v must be powers of 2"
+        _envelope(Q, K, V)
+
+        O = torch.empty((batch_size, num_heads, seq_len, d_v), device=Q.device, dtype=Q.dtype)
+        L = torch.empty((batch_size, num_heads, seq_len), device=Q.device, dtype=torch.float32)
+        q, k, v = _vec(Q), _vec(K), _vec(V)
+        lib = _lib.load()
+        nbytes = lib.mi_fa2_fwd_workspace_size(batch_size, num_heads, num_kv_heads, seq_len,
+                                               seq_len_k, d)
+        ws = _workspace(nbytes, Q.device)
+        with torch.cuda.device(Q.device):
+            _lib.check(lib.mi_fa2_fwd(
+                _lib.DTYPES[Q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(),
+                L.data_ptr(), kv_lens.data_ptr() if kv_lens is not None else None,
+                batch_size, num_heads, num_kv_heads, seq_len, seq_len_k, d,
+                _strides(q), _strides(k), _strides(v), _strides(O), _strides(L),
+                int(bool(is_causal)), sm_scale,
+                ws.data_ptr() if ws is not None else None, nbytes, _lib.stream_of(Q)))
+
+        ctx.save_for_backward(Q, K, V, O, L)
+        ctx.is_causal = is_causal
+        ctx.scale = sm_scale
+        return O
+
+
+def fa2_forward(Q, K, V, is_causal=False, kv_lens=None, return_lse=False):
+    """Functional form of FlashAttention2Function.apply; optionally also returns the fp32 LSE."""
+    if not return_lse:
+        return FlashAttention2Function.apply(Q, K, V, is_causal, kv_lens)
+    with torch.no_grad():
+        ctx = _Ctx()
+        O = FlashAttention2Function.forward(ctx, Q, K, V, is_causal, kv_lens)
+    return O, ctx.saved[4]
+
+
+class _Ctx:
+    def save_for_backward(self, *t):
+        self.saved = t
+
+
+def fa2_paged(q, k_pool, v_pool, block_table, kv_lens, *, block_size=16, max_kv_len=None,
+              is_causal=None, return_lse=False):
+    """Attention over K/V held in a paged pool, read in-kernel through a block table.
+
+    q            [B, Hq, T, 128]   this step's queries (T = 1 for decode)
+    k_pool/v_pool [num_blocks*block_size, Hkv, 128]: one layer of KVCache.buf (kv_cache.py:20-22)
+    block_table  [B, W] int32: row b's token p is at slot block_table[b, p // block_size] *
+                 block_size + p % block_size (kv_cache.py:15-16)
+    kv_lens      [B] int32: keys per row including this step's T (model.py:175)
+    max_kv_len   host-side upper bound of kv_lens (default W * block_size)
+    is_causal    default T > 1, as model.py:185 sets it; bottom-right aligned per row
+    Returns O [B, Hq, T, 128] (and the fp32 LSE [B, Hq, T] if return_lse).
+    """
+    assert q.is_cuda and k_pool.is_cuda and v_pool.is_cuda, "q and the pools must be GPU tensors"
+    B, Hq, T, d = q.shape
+    assert k_pool.dim() == 3 and k_pool.shape == v_pool.shape, "pools are [slots, Hkv, d]"
+    assert k_pool.stride() == v_pool.stride(), "k_pool and v_pool must share strides"
+    Hkv = k_pool.shape[1]
+    assert Hq % Hkv == 0, "query heads must be a multiple of kv heads (GQA)"
+    assert block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == B
+    assert kv_lens.dtype == torch.int32 and kv_lens.shape == (B,)
+    assert block_table.stride(-1) == 1, "block_table rows must be contiguous"
+    assert block_size >= 16 and block_size & (block_size - 1) == 0, "block_size: power of 2, >= 16"
+    assert k_pool.shape[0] % block_size == 0, "pool slots must be whole blocks"
+    _envelope(q, k_pool, v_pool)
+    if max_kv_len is None:
+        max_kv_len = block_table.shape[1] * block_size
+    # kv_lens are clamped to max_kv_len in-kernel, so this bound keeps every table read in range
+    assert 0 <= max_kv_len <= block_table.shape[1] * block_size, \
+        "max_kv_len exceeds what the block table can address"
+    if is_causal is None:
+        is_causal = T > 1
+    q = _vec(q)
+    assert _dims_ok(k_pool) and _dims_ok(v_pool), "pools need 16-byte aligned token rows"
+    O = torch.empty((B, Hq, T, d), device=q.device, dtype=q.dtype)
+    L = torch.empty((B, Hq, T), device=q.device, dtype=torch.float32)
+    lib = _lib.load()
+    nbytes = lib.mi_fa2_fwd_paged_workspace_size(B, Hq, Hkv, T, max_kv_len, d)
+    ws = _workspace(nbytes, q.device)
+    pool_strides = (_lib.ctypes.c_int64 * 2)(*k_pool.stride()[:2])
+    with torch.cuda.device(q.device):
+        _lib.check(lib.mi_fa2_fwd_paged(
+            _lib.DTYPES[q.dtype], q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), O.data_ptr(),
+            L.data_ptr(), block_table.data_ptr(), block_table.stride(0), kv_lens.data_ptr(),
+            B, Hq, Hkv, T, int(max_kv_len), d, block_size, k_pool.shape[0] // block_size,
+            _strides(q), pool_strides, _strides(O), _strides(L), int(bool(is_causal)),
+            1.0 / math.sqrt(d), ws.data_ptr() if ws is not None else None, nbytes,
+            _lib.stream_of(q)))
+    return (O, L) if return_lse else O
+
+
+def fa2_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, is_causal=False,
+               return_lse=False):
+    """Attention over a ragged batch packed back to back.
+
+    q [total_q, Hq, 128], k/v [total_k, Hkv, 128]; cu_seqlens_q/k [B+1] int32 prefix offsets;
+    row b = q[cu_q[b]:cu_q[b+1]] against k/v[cu_k[b]:cu_k[b+1]], causal aligned to the row's end.
+    Returns O [total_q, Hq, 128] (and the fp32 LSE [Hq, total_q] if return_lse).
+    """
+    assert q.is_cuda and k.is_cuda and v.is_cuda, "q, k and v must be GPU tensors"
+    assert q.dim() == 3 and k.dim() == 3 and k.shape[:-1] == v.shape[:-1]
+    assert cu_seqlens_q.dtype == torch.int32 and cu_seqlens_k.dtype == torch.int32
+    B = cu_seqlens_q.shape[0] - 1
+    assert cu_seqlens_k.shape[0] == B + 1
+    total_q, Hq, d = q.shape
+    Hkv = k.shape[1]
+    assert Hq % Hkv == 0, "query heads must be a multiple of kv heads (GQA)"
+    _envelope(q, k, v)
+    q, k, v = _vec(q), _vec(k), _vec(v)
+    O = torch.empty((total_q, Hq, d), device=q.device, dtype=q.dtype)
+    L = torch.empty((Hq, total_q), device=q.device, dtype=torch.float32)
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        _lib.check(lib.mi_fa2_fwd_varlen(
+            _lib.DTYPES[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(),
+            L.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), B, Hq, Hkv,
+            int(max_seqlen_q), d, _strides(q), _strides(k), _strides(v), _strides(O),
+            _strides(L), int(bool(is_causal)), 1.0 / math.sqrt(d), _lib.stream_of(q)))
+    return (O, L) if return_lse else O

@@ -1,0 +1,25 @@
+"""CPU oracle of the attention hot path.  TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package, and
+only as the checker (or the timed CPU baseline), never as part of the product path.
+
+Contents (each function cites the reference lines it restates; nothing is imported from the
+reference):
+  sdpa.attention_ref     fp32 SDPA with repeat_kv and an explicit bottom-right causal mask, run
+                         per row on the row's real keys: kernels/test_fa2.py:28-35,54-57 and the
+                         model's CPU fallback model.py:70-75,102-107.
+  sdpa.lse_ref           log-sum-exp of the scaled scores, the L the reference kernel computes
+                         (kernels/fa2.py:155-158).
+  sdpa.varlen_ref        the same per row of a packed batch.
+  paged.gather_dense     the paged cache's slot arithmetic and dense gather (kv_cache.py:15-16,
+                         93-98, 117-121).
+  paged.build_pool       a KVCache-layout pool + per-row block tables from dense K/V.
+  brute.attention_f64    float64 loops over (row, head, query, key): the textbook definition,
+                         used to pin sdpa.attention_ref on small shapes.
+
+The seeded workload generators are not part of the oracle: they live in the package
+(my-inference-engine_amd/workloads.py) because bench.py's GPU leg needs them too.
+
+Parity status: every function above is pinned by tests/test_oracle.py (fp64 brute force, closed
+forms, GQA/permutation/padding invariants).  None is "parity unpinned".
+"""

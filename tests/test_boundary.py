@@ -1,0 +1,110 @@
+"""CPU checks of the drop-in boundary: libmi_fa2.so loads, exports exactly what include/mi_fa2.h
+declares, validates its arguments before touching the GPU, and the Python mirror of
+FlashAttention2Function (kernels/fa2.py:164-214) raises like the reference on bad inputs.
+No kernel is launched here."""
+import ctypes
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+from kernels import _lib, fa2
+
+HEADER = ROOT / "include" / "mi_fa2.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"MI_FA2_API\s+[\w\s\*]+?\b(mi_fa2_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) == 7
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.SIGNATURES)
+
+
+def test_library_exports_nothing_else():
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = sorted(line.split()[-1] for line in out.splitlines() if " T " in line)
+    assert exported == declared_symbols()
+
+
+def test_version_and_clean_error_state():
+    lib = _lib.load()
+    assert lib.mi_fa2_version().decode().startswith("mi_fa2 ")
+    assert "gfx950" in lib.mi_fa2_version().decode()
+
+
+def test_workspace_sizes():
+    lib = _lib.load()
+    # prefill needs none
+    assert lib.mi_fa2_fwd_workspace_size(1, 12, 2, 4096, 4096, 128) == 0
+    # a decode step with long rows needs [B, Hq, splits] x (128 + 2) fp32
+    n = lib.mi_fa2_fwd_paged_workspace_size(64, 12, 2, 1, 8192, 128)
+    assert n > 0 and n % (12 * 64 * 130 * 4) == 0
+    # a single short row fits in one split: no workspace
+    assert lib.mi_fa2_fwd_workspace_size(1, 12, 2, 1, 100, 128) == 0
+
+
+def _fwd(lib, **over):
+    args = dict(dtype=0, q=16, k=16, v=16, o=16, lse=None, kv_lens=None, batch=1, heads_q=12,
+                heads_kv=2, seqlen_q=8, seqlen_k=8, head_dim=128)
+    args.update(over)
+    st = (ctypes.c_int64 * 4)(8192, 1024, 128, 1)
+    return lib.mi_fa2_fwd(args["dtype"], args["q"], args["k"], args["v"], args["o"], args["lse"],
+                          args["kv_lens"], args["batch"], args["heads_q"], args["heads_kv"],
+                          args["seqlen_q"], args["seqlen_k"], args["head_dim"],
+                          over.get("q_strides", st), st, st, st, None, 1, 0.1, None, 0, None)
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(head_dim=64), 2, "head_dim 64"),
+    (dict(dtype=7), 2, "dtype"),
+    (dict(heads_q=12, heads_kv=5), 1, "multiple"),
+    (dict(q=None), 1, "q is NULL"),
+    (dict(q=24), 1, "16-byte aligned"),
+    (dict(seqlen_q=-1), 1, "bad lengths"),
+    (dict(q_strides=(ctypes.c_int64 * 4)(8192, 1024, 100, 1)), 1, "multiple of 8"),
+])
+def test_c_abi_rejects_bad_arguments_before_any_launch(over, status, msg):
+    lib = _lib.load()
+    assert _fwd(lib, **over) == status
+    assert msg in lib.mi_fa2_last_error().decode()
+
+
+def test_paged_rejects_bad_block_size():
+    lib = _lib.load()
+    st = (ctypes.c_int64 * 4)(1536, 128, 1536, 1)
+    ps = (ctypes.c_int64 * 2)(256, 128)
+    rc = lib.mi_fa2_fwd_paged(0, 16, 16, 16, 16, None, 16, 8, 16, 1, 12, 2, 1, 64, 128, 24, 10,
+                              st, ps, st, None, 0, 0.1, None, 0, None)
+    assert rc == 2 and "block_size" in lib.mi_fa2_last_error().decode()
+
+
+def test_zero_sized_calls_are_no_ops():
+    lib = _lib.load()
+    assert _fwd(lib, batch=0) == 0
+    assert _fwd(lib, seqlen_q=0) == 0
+
+
+def test_python_mirror_asserts_like_the_reference():
+    q = torch.randn(1, 12, 4, 128, dtype=torch.bfloat16)
+    k = torch.randn(1, 2, 4, 128, dtype=torch.bfloat16)
+    # CPU tensors: the reference asserts is_cuda (kernels/fa2.py:177)
+    with pytest.raises(AssertionError):
+        fa2.FlashAttention2Function.apply(q, k, k, True, None)
+
+
+def test_stride_helper_zeroes_size_one_dims():
+    t = torch.empty(3, 1, 5, 128)[:, :, :, :]
+    s = list(fa2._strides(t))
+    assert s == [640, 0, 128, 1]
+    assert fa2._dims_ok(torch.empty(2, 12, 7, 128))
+    assert not fa2._dims_ok(torch.empty(2, 12, 7, 128).transpose(-1, -2))

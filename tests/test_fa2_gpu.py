@@ -1,0 +1,310 @@
+"""GPU parity of the HIP kernels against the CPU oracle, through the C ABI (libmi_fa2.so).
+
+Tolerance (bf16/fp16 outputs vs the fp32 oracle): max-abs error < 1e-2 and mean-abs error < 1e-3.
+The reference's own test allows max-abs 2e-2 (kernels/test_fa2.py:25).
+"""
+import math
+
+import pytest
+import torch
+
+from conftest import announce
+from kernels import _lib
+from kernels.fa2 import FlashAttention2Function, fa2_forward, fa2_paged, fa2_varlen
+from oracle import paged as opaged
+from oracle import sdpa
+import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 1e-2
+MEAN_ABS = 1e-3
+PAD_VALUE = 100.0  # kernels/test_fa2.py:24
+DEV = "cuda"
+
+
+def check_close(out, ref, max_abs=MAX_ABS, mean_abs=MEAN_ABS, what=""):
+    out = out.float().cpu()
+    ref = ref.float().cpu()
+    assert out.shape == ref.shape, (out.shape, ref.shape)
+    assert torch.isfinite(out).all(), f"{what}: non-finite output"
+    err = (out - ref).abs()
+    assert err.max().item() < max_abs, f"{what}: max-abs {err.max().item():.3e}"
+    assert err.mean().item() < mean_abs, f"{what}: mean-abs {err.mean().item():.3e}"
+    return err.max().item()
+
+
+# The reference's known-answer cases (kernels/test_fa2.py:17-23): (name, T, kv_lens, causal).
+CASES = [
+    ("prefill", 300, [300, 300], True),
+    ("decode", 1, [1000, 1000], False),
+    ("chunked", 64, [500, 500], True),
+    ("ragged decode", 1, [1000, 37, 512, 1], False),
+    ("ragged prefill", 16, [16, 300, 100], True),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("case", CASES, ids=[c[0].replace(" ", "_") for c in CASES])
+def test_reference_cases(case, dtype):
+    name, T, lens, causal = case
+    B, S = len(lens), max(lens)
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(B, 12, T, 128, generator=g).to(dtype)
+    k = torch.randn(B, 2, S, 128, generator=g).to(dtype)
+    v = torch.randn(B, 2, S, 128, generator=g).to(dtype)
+    for b, n in enumerate(lens):
+        k[b, :, n:] = PAD_VALUE
+        v[b, :, n:] = PAD_VALUE
+    announce(f"[gpu] reference case {name} {dtype}")
+    kv_lens = torch.tensor(lens, dtype=torch.int32)
+    out = FlashAttention2Function.apply(q.to(DEV), k.to(DEV), v.to(DEV), causal, kv_lens.to(DEV))
+    torch.cuda.synchronize()
+    ref = sdpa.attention_ref(q, k, v, causal, lens)
+    check_close(out, ref, what=name)
+
+
+def test_lse_matches_oracle():
+    g = torch.Generator().manual_seed(1)
+    lens = [77, 300, 5]
+    q = torch.randn(3, 12, 40, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(3, 2, 300, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(3, 2, 300, 128, generator=g).to(torch.bfloat16)
+    announce("[gpu] lse prefill")
+    out, lse = fa2_forward(q.to(DEV), k.to(DEV), v.to(DEV), True,
+                           torch.tensor(lens, dtype=torch.int32, device=DEV), return_lse=True)
+    torch.cuda.synchronize()
+    want = sdpa.lse_ref(q, k, True, lens)
+    fin = torch.isfinite(want)
+    assert torch.equal(fin, torch.isfinite(lse.cpu()))  # row 2 has queries that see no key
+    assert (lse.cpu()[fin] - want[fin]).abs().max().item() < 1e-3
+    check_close(out, sdpa.attention_ref(q, k, v, True, lens), what="lse case output")
+    # decode (split-KV + combine) LSE
+    announce("[gpu] lse decode")
+    qd = q[:, :, :1].contiguous()
+    out, lse = fa2_forward(qd.to(DEV), k.to(DEV), v.to(DEV), False,
+                           torch.tensor(lens, dtype=torch.int32, device=DEV), return_lse=True)
+    torch.cuda.synchronize()
+    want = sdpa.lse_ref(qd, k, False, lens)
+    assert (lse.cpu() - want).abs().max().item() < 1e-3
+
+
+def test_prefill_seq4096_causal():
+    q, k, v = wl.prefill_single(4096, seed=0)
+    announce("[gpu] prefill 1x12x4096 causal")
+    out = FlashAttention2Function.apply(q.to(DEV), k.to(DEV), v.to(DEV), True, None)
+    torch.cuda.synchronize()
+    check_close(out, sdpa.attention_ref(q, k, v, True), what="prefill 4096")
+
+
+def test_ragged_varlen_prefill():
+    q, k, v, lens, cu = wl.prefill_ragged(seed=0)
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=DEV)
+    announce(f"[gpu] varlen prefill lens={lens}")
+    out = fa2_varlen(q.to(DEV), k.to(DEV), v.to(DEV), cu_t, cu_t, max(lens), is_causal=True)
+    torch.cuda.synchronize()
+    check_close(out, sdpa.varlen_ref(q, k, v, cu, cu, True), what="varlen")
+
+
+def test_varlen_with_longer_keys_than_queries():
+    # chunked prefill rows: each row's queries are the last T_b of its kv_b keys
+    g = torch.Generator().manual_seed(2)
+    qlens, klens = [5, 130, 1, 64], [40, 130, 300, 64]
+    cq, ck = [0], [0]
+    for a, b in zip(qlens, klens):
+        cq.append(cq[-1] + a)
+        ck.append(ck[-1] + b)
+    q = torch.randn(cq[-1], 12, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(ck[-1], 2, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(ck[-1], 2, 128, generator=g).to(torch.bfloat16)
+    announce("[gpu] varlen q<k")
+    out = fa2_varlen(q.to(DEV), k.to(DEV), v.to(DEV), torch.tensor(cq, dtype=torch.int32, device=DEV),
+                     torch.tensor(ck, dtype=torch.int32, device=DEV), max(qlens), is_causal=True)
+    torch.cuda.synchronize()
+    check_close(out, sdpa.varlen_ref(q, k, v, cq, ck, True), what="varlen q<k")
+
+
+def _paged_ref(q, k_pool, v_pool, tables, kv_lens, bs, causal):
+    S = max(kv_lens)
+    kd = opaged.gather_dense(k_pool, tables, S, bs)
+    vd = opaged.gather_dense(v_pool, tables, S, bs)
+    return sdpa.attention_ref(q, kd, vd, causal, kv_lens)
+
+
+def test_paged_decode_64_rows():
+    q, kp, vp, tables, lens = wl.decode_paged(seed=0)
+    bt = wl.table_tensor(tables)
+    announce(f"[gpu] paged decode 64 rows, max len {max(lens)}")
+    out = fa2_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), bt.to(DEV),
+                    torch.tensor(lens, dtype=torch.int32, device=DEV))
+    torch.cuda.synchronize()
+    check_close(out, _paged_ref(q, kp, vp, tables, lens, 16, False), what="paged decode")
+
+
+def test_paged_decode_block_permutation_invariance():
+    # the same logical rows stored in differently permuted blocks give bit-identical outputs
+    q, kp, vp, tables, lens = wl.decode_paged(n_rows=16, lo=1, hi=3000, seed=3, spare_blocks=40)
+    g = torch.Generator().manual_seed(9)
+    perm = torch.randperm(kp.shape[0] // 16, generator=g)
+    # new block id of old block i is perm[i]: move the data accordingly
+    kp2 = torch.empty_like(kp).view(-1, 16, 2, 128)
+    vp2 = torch.empty_like(vp).view(-1, 16, 2, 128)
+    kp2[perm] = kp.view(-1, 16, 2, 128)
+    vp2[perm] = vp.view(-1, 16, 2, 128)
+    tables2 = [[int(perm[b]) for b in t] for t in tables]
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    announce("[gpu] paged decode permutation")
+    o1 = fa2_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), wl.table_tensor(tables).to(DEV), lens_t)
+    o2 = fa2_paged(q.to(DEV), kp2.view(-1, 2, 128).to(DEV), vp2.view(-1, 2, 128).to(DEV),
+                   wl.table_tensor(tables2).to(DEV), lens_t)
+    torch.cuda.synchronize()
+    assert torch.equal(o1.cpu(), o2.cpu())
+    check_close(o1, _paged_ref(q, kp, vp, tables, lens, 16, False), what="paged perm")
+
+
+def test_paged_decode_equals_dense_decode_bitwise():
+    q, kp, vp, tables, lens = wl.decode_paged(n_rows=8, lo=1, hi=2000, seed=4)
+    S = max(lens)
+    kd = opaged.gather_dense(kp, tables, S, 16).contiguous()
+    vd = opaged.gather_dense(vp, tables, S, 16).contiguous()
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    announce("[gpu] paged vs dense decode")
+    o_dense = FlashAttention2Function.apply(q.to(DEV), kd.to(DEV), vd.to(DEV), False, lens_t)
+    o_paged = fa2_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), wl.table_tensor(tables).to(DEV), lens_t,
+                        max_kv_len=S)
+    torch.cuda.synchronize()
+    assert torch.equal(o_dense.cpu(), o_paged.cpu())
+
+
+def test_paged_prefill_over_cached_context():
+    # a new turn of T tokens appended to chats that already hold context (kv_lens include T)
+    g = torch.Generator().manual_seed(5)
+    T, lens, bs = 37, [100, 37, 250], 16
+    num_blocks = 64
+    tables = opaged.random_tables(lens, bs, num_blocks, g)
+    kp = torch.randn(num_blocks * bs, 2, 128, generator=g).to(torch.bfloat16)
+    vp = torch.randn(num_blocks * bs, 2, 128, generator=g).to(torch.bfloat16)
+    q = torch.randn(3, 12, T, 128, generator=g).to(torch.bfloat16)
+    announce("[gpu] paged prefill")
+    out = fa2_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), wl.table_tensor(tables).to(DEV),
+                    torch.tensor(lens, dtype=torch.int32, device=DEV))
+    torch.cuda.synchronize()
+    check_close(out, _paged_ref(q, kp, vp, tables, lens, bs, True), what="paged prefill")
+
+
+def test_paged_block_size_32():
+    g = torch.Generator().manual_seed(6)
+    lens, bs = [33, 700, 64], 32
+    num_blocks = 40
+    tables = opaged.random_tables(lens, bs, num_blocks, g)
+    kp = torch.randn(num_blocks * bs, 2, 128, generator=g).to(torch.bfloat16)
+    vp = torch.randn(num_blocks * bs, 2, 128, generator=g).to(torch.bfloat16)
+    q = torch.randn(3, 12, 1, 128, generator=g).to(torch.bfloat16)
+    announce("[gpu] paged block_size 32")
+    out = fa2_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), wl.table_tensor(tables).to(DEV),
+                    torch.tensor(lens, dtype=torch.int32, device=DEV), block_size=bs)
+    torch.cuda.synchronize()
+    check_close(out, _paged_ref(q, kp, vp, tables, lens, bs, False), what="bs32")
+
+
+def test_empty_rows_and_queries_without_keys_give_zero():
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(3, 12, 20, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(3, 2, 12, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(3, 2, 12, 128, generator=g).to(torch.bfloat16)
+    lens = [0, 12, 5]  # row 0: no keys; rows 1-2: T > kv_len, early queries see nothing
+    announce("[gpu] empty rows")
+    out = FlashAttention2Function.apply(q.to(DEV), k.to(DEV), v.to(DEV), True,
+                                        torch.tensor(lens, dtype=torch.int32, device=DEV))
+    torch.cuda.synchronize()
+    ref = sdpa.attention_ref(q, k, v, True, lens)
+    assert torch.equal(out[0].cpu(), torch.zeros_like(out[0].cpu()))
+    assert torch.equal(out[2, :, :15].cpu(), torch.zeros(12, 15, 128, dtype=torch.bfloat16))
+    check_close(out, ref, what="empty rows")
+
+
+def test_nan_padding_never_leaks():
+    g = torch.Generator().manual_seed(8)
+    lens = [70, 129]
+    for T, causal in [(1, False), (9, True)]:
+        q = torch.randn(2, 12, T, 128, generator=g).to(torch.bfloat16)
+        k = torch.randn(2, 2, 200, 128, generator=g).to(torch.bfloat16)
+        v = torch.randn(2, 2, 200, 128, generator=g).to(torch.bfloat16)
+        for b, n in enumerate(lens):
+            k[b, :, n:] = float("nan")
+            v[b, :, n:] = float("inf")
+        announce(f"[gpu] nan padding T={T}")
+        out = FlashAttention2Function.apply(q.to(DEV), k.to(DEV), v.to(DEV), causal,
+                                            torch.tensor(lens, dtype=torch.int32, device=DEV))
+        torch.cuda.synchronize()
+        check_close(out, sdpa.attention_ref(q, k, v, causal, lens), what=f"nan pad T={T}")
+
+
+def test_strided_inputs_like_model_py():
+    # model.py:88-90: q/k/v come from a [B, T, H*d] projection viewed and transposed
+    g = torch.Generator().manual_seed(10)
+    B, T = 2, 70
+    x = torch.randn(B, T, 12 * 128 + 2 * 2 * 128, generator=g).to(torch.bfloat16).to(DEV)
+    q = x[..., :1536].view(B, T, 12, 128).transpose(1, 2)
+    k = x[..., 1536:1792].view(B, T, 2, 128).transpose(1, 2)
+    v = x[..., 1792:].view(B, T, 2, 128).transpose(1, 2)
+    assert not q.is_contiguous()
+    announce("[gpu] strided inputs")
+    out = FlashAttention2Function.apply(q, k, v, True, None)
+    torch.cuda.synchronize()
+    check_close(out, sdpa.attention_ref(q.cpu(), k.cpu(), v.cpu(), True), what="strided")
+
+
+@pytest.mark.parametrize("T", [2, 31, 129, 200])
+def test_odd_query_counts(T):
+    g = torch.Generator().manual_seed(11 + T)
+    lens = [T + 3, T + 60]
+    q = torch.randn(2, 12, T, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(2, 2, max(lens), 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(2, 2, max(lens), 128, generator=g).to(torch.bfloat16)
+    announce(f"[gpu] odd T={T}")
+    out = FlashAttention2Function.apply(q.to(DEV), k.to(DEV), v.to(DEV), True,
+                                        torch.tensor(lens, dtype=torch.int32, device=DEV))
+    torch.cuda.synchronize()
+    check_close(out, sdpa.attention_ref(q, k, v, True, lens), what=f"T={T}")
+
+
+def test_mha_and_other_group_sizes():
+    g = torch.Generator().manual_seed(12)
+    for hq, hkv in [(4, 4), (16, 1), (32, 2)]:
+        for T in (1, 50):
+            q = torch.randn(2, hq, T, 128, generator=g).to(torch.bfloat16)
+            k = torch.randn(2, hkv, 90, 128, generator=g).to(torch.bfloat16)
+            v = torch.randn(2, hkv, 90, 128, generator=g).to(torch.bfloat16)
+            announce(f"[gpu] heads {hq}/{hkv} T={T}")
+            out = FlashAttention2Function.apply(q.to(DEV), k.to(DEV), v.to(DEV), True, None)
+            torch.cuda.synchronize()
+            check_close(out, sdpa.attention_ref(q, k, v, True), what=f"{hq}/{hkv} T={T}")
+
+
+def test_repeat_calls_are_bitwise_deterministic():
+    q, k, v = wl.prefill_single(1024, seed=13)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    announce("[gpu] determinism")
+    a = FlashAttention2Function.apply(q, k, v, True, None)
+    b = FlashAttention2Function.apply(q, k, v, True, None)
+    qd, kp, vp, tables, lens = wl.decode_paged(n_rows=8, seed=13)
+    args = (qd.to(DEV), kp.to(DEV), vp.to(DEV), wl.table_tensor(tables).to(DEV),
+            torch.tensor(lens, dtype=torch.int32, device=DEV))
+    c, d = fa2_paged(*args), fa2_paged(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(c, d)
+
+
+def test_workspace_too_small_is_an_error():
+    lib = _lib.load()
+    q = torch.zeros(64, 12, 1, 128, dtype=torch.bfloat16, device=DEV)
+    k = torch.zeros(64, 2, 8192, 128, dtype=torch.bfloat16, device=DEV)
+    need = lib.mi_fa2_fwd_workspace_size(64, 12, 2, 1, 8192, 128)
+    assert need > 0
+    o = torch.empty_like(q)
+    st = lambda t: (_lib.ctypes.c_int64 * 4)(*t.stride())
+    rc = lib.mi_fa2_fwd(0, q.data_ptr(), k.data_ptr(), k.data_ptr(), o.data_ptr(), None, None, 64,
+                        12, 2, 1, 8192, 128, st(q), st(k), st(k), st(o), None, 0,
+                        1 / math.sqrt(128), None, 0, _lib.stream_of(q))
+    assert rc == 3 and "workspace" in lib.mi_fa2_last_error().decode()
