@@ -1,0 +1,230 @@
+"""Benchmark of the MI355X attention hot path; prints one JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
+
+A "step" is one call of the hot path on one batch of synthetic input, inputs resident in HBM:
+
+  headline (value): causal prefill attention, 1 sequence x 12 q heads / 2 kv heads x 4096 tokens x
+      head_dim 128, bf16 -> TFLOP/s (algorithmic flops 4*d*H*L(L+1)/2 over the measured time)
+  secondary: paged decode, 64 rows with kv_len ~ U[128, 8192] in 16-token blocks under a permuted
+      block table -> HBM GB/s (every visible K/V byte once + q, o, block table, lengths), with
+      enough pool copies rotated per step that no step finds its K/V in the 256 MB MALL;
+      ragged packed prefill, 16 sequences with L ~ U[16, 1024] -> TFLOP/s.
+
+Timing: W untimed warmup steps, then torch.cuda.synchronize(); a HIP event pair on the stream the
+kernels are launched on brackets exactly K steps; synchronize.  The per-launch duration is the
+event time / K.  The CPU baseline is the fp32 SDPA oracle (the reference's fallback path) on the
+same inputs, on this host's cores, median of 5 runs.
+
+One GPU only: --gpus N > 1 exits with a message.
+"""
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+PKG = ROOT / "my-inference-engine_amd"
+for _p in (str(ROOT), str(PKG)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "prefill attn TFLOP/s + paged-decode attn HBM GB/s; e2e tok/s at 16 chats"
+PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 flop/clk/CU
+PEAK_HBM_GBS = 8000.0      # HBM3E
+
+
+def _time_gpu(fn, steps, warmup):
+    """Average ms per call of fn() over exactly `steps` calls, HIP events on the current stream."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def bench_prefill(steps, warmup, seq_len=4096):
+    import torch
+    import workloads as wl
+    from kernels.fa2 import FlashAttention2Function
+    q, k, v = (t.cuda() for t in wl.prefill_single(seq_len, seed=0))
+    ms = _time_gpu(lambda i=0: FlashAttention2Function.apply(q, k, v, True, None), steps, warmup)
+    flops = wl.causal_prefill_flops([seq_len])
+    return ms, flops
+
+
+def bench_ragged(steps, warmup):
+    import torch
+    import workloads as wl
+    from kernels.fa2 import fa2_varlen
+    q, k, v, lens, cu = wl.prefill_ragged(seed=0)
+    q, k, v = q.cuda(), k.cuda(), v.cuda()
+    cu_t = torch.tensor(cu, dtype=torch.int32, device="cuda")
+    mx = max(lens)
+    ms = _time_gpu(lambda i=0: fa2_varlen(q, k, v, cu_t, cu_t, mx, is_causal=True), steps, warmup)
+    return ms, wl.causal_prefill_flops(lens), lens
+
+
+def bench_decode(steps, warmup, rotate_bytes=2 << 30):
+    import torch
+    import workloads as wl
+    from kernels.fa2 import fa2_paged
+    q, kp, vp, tables, lens = wl.decode_paged(seed=0)
+    bt = wl.table_tensor(tables).cuda()
+    lens_t = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    q = q.cuda()
+    pool_bytes = 2 * kp.numel() * kp.element_size()
+    copies = max(2, math.ceil(rotate_bytes / pool_bytes))
+    pools = []
+    for _ in range(copies):
+        pools.append((kp.cuda(), vp.cuda()))
+    max_kv = bt.shape[1] * 16
+
+    def step(i=0):
+        kpc, vpc = pools[i % copies]
+        return fa2_paged(q, kpc, vpc, bt, lens_t, max_kv_len=max_kv)
+
+    ms = _time_gpu(step, steps, warmup)
+    return ms, wl.decode_bytes(lens), lens, copies
+
+
+def cpu_prefill_baseline(seq_len=4096, runs=5):
+    import torch
+    import workloads as wl
+    from oracle import sdpa
+    q, k, v = (t.float() for t in wl.prefill_single(seq_len, seed=0))
+    sdpa.attention_ref(q, k, v, True)  # warm up
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        sdpa.attention_ref(q, k, v, True)
+        times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    return wl.causal_prefill_flops([seq_len]) / sec / 1e12, torch.get_num_threads(), sec
+
+
+def cpu_decode_baseline(runs=3):
+    """The reference's CPU decode path: dense gather of every row's blocks (kv_cache.py:117-121)
+    then fp32 SDPA per row; a 16-row sample of the 64-row workload."""
+    import torch
+    import workloads as wl
+    from oracle import paged as opaged
+    from oracle import sdpa
+    q, kp, vp, tables, lens = wl.decode_paged(seed=0)
+    q, kp, vp = q[:16].float(), kp.float(), vp.float()
+    tables, lens = tables[:16], lens[:16]
+    S = max(lens)
+
+    def run():
+        kd = opaged.gather_dense(kp, tables, S, 16)
+        vd = opaged.gather_dense(vp, tables, S, 16)
+        return sdpa.attention_ref(q, kd, vd, False, lens)
+
+    run()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    return wl.decode_bytes(lens) / sec / 1e9, torch.get_num_threads(), sec
+
+
+def read_traffic(name):
+    """HBM bytes per launch recorded by the rocprofv3 --pmc summaries under profiles/, if any."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    try:
+        return json.loads(path.read_text()).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-secondary", action="store_true", help="prefill headline only")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build's hot path runs on a single MI355X "
+              f"(--gpus {args.gpus} is not supported)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+
+    ms, flops = bench_prefill(args.steps, args.warmup)
+    tflops = flops / (ms * 1e-3) / 1e12
+    out = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "causal prefill attention, 1 sequence x 12 q heads / 2 kv heads x "
+                               "4096 tokens x head_dim 128, bf16, N(0,1) seed 0",
+                   "flops_per_step": flops},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": read_traffic("fa2_prefill_kernel")},
+    }
+    if not args.no_cpu:
+        cpu_tflops, cores, sec = cpu_prefill_baseline()
+        out["cpu_baseline"] = {"value": round(cpu_tflops, 4), "unit": "TFLOP/s", "cores": cores,
+                               "kind": "port",
+                               "sample": f"the same 1x12x4096 causal prefill in fp32 through the "
+                                         f"SDPA oracle, median of 5 runs ({sec:.3f} s each)",
+                               "host_cpu_count": os.cpu_count()}
+    if not args.no_secondary:
+        dms, dbytes, lens, copies = bench_decode(args.steps, args.warmup)
+        gbs = dbytes / (dms * 1e-3) / 1e9
+        dec = {"metric": "paged-decode attn HBM GB/s", "value": round(gbs, 1), "unit": "GB/s",
+               "ms_per_step": round(dms, 5), "bytes_per_step": dbytes,
+               "workload": f"paged decode, 64 rows x 12q/2kv x head_dim 128, kv_len U[128,8192] "
+                           f"(sum {sum(lens)}), 16-token blocks, permuted block table, bf16; "
+                           f"{copies} pool copies rotated so no step hits the MALL",
+               "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                            "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                            "traffic": read_traffic("fa2_decode_kernel")}}
+        if not args.no_cpu:
+            cgbs, cores, sec = cpu_decode_baseline()
+            dec["cpu_baseline"] = {"value": round(cgbs, 3), "unit": "GB/s", "cores": cores,
+                                   "kind": "port",
+                                   "sample": f"16 of the 64 rows: dense gather + fp32 SDPA, median "
+                                             f"of 3 runs ({sec:.3f} s each)"}
+        rms, rflops, rlens = bench_ragged(args.steps, args.warmup)
+        rt = rflops / (rms * 1e-3) / 1e12
+        rag = {"metric": "ragged varlen prefill attn TFLOP/s", "value": round(rt, 2),
+               "unit": "TFLOP/s", "ms_per_step": round(rms, 5), "flops_per_step": rflops,
+               "workload": f"16 packed causal sequences, L ~ U[16,1024] (sum {sum(rlens)}), "
+                           f"12q/2kv, head_dim 128, bf16",
+               "roofline": {"bound": "mfma", "achieved": round(rt, 2), "peak": PEAK_BF16_TFLOPS,
+                            "unit": "TFLOP/s", "frac": round(rt / PEAK_BF16_TFLOPS, 4)}}
+        out["secondary"] = [dec, rag]
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
