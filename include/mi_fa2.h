@@ -24,7 +24,8 @@
  *     Triton kernel would produce 0/0 = NaN there.
  *   - Launches are asynchronous on `stream` (a hipStream_t); nothing is synchronised and nothing
  *     is allocated.  Entry points that need scratch take a caller-owned workspace whose size the
- *     matching *_workspace_size() returns.
+ *     matching *_workspace_size() returns; its contents need no initialisation.  Calls that
+ *     overlap in time (other streams) must not share one workspace.
  *   - Return value: MI_FA2_OK (0) or an error code; mi_fa2_last_error() then describes it.
  */
 #ifndef MI_FA2_H

@@ -6,6 +6,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 
 #include "fa2_common.h"
 
@@ -37,9 +38,17 @@ int ok() {
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
 // Keys per split of the decode kernel: 4 waves x 32 keys at least, doubled until the grid holds at
-// most ~4096 work-groups (about 16 per CU on 256 CUs), so long rows get enough parallelism while a
-// split stays long enough to amortise its set-up and partial write.
+// most 4096 work-groups (16 per CU on 256 CUs, about half of them empty for rows shorter than the
+// longest), so long rows get enough parallelism while every wave still walks a few steps.  On
+// the 64-row U[128,8192] decode 256 keys measured best (128: -4%, 512: -15%).  MI_FA2_DECODE_CHUNK (a multiple of 128) overrides it,
+// for tuning sweeps.
 int decode_chunk(int64_t batch, int64_t heads_kv, int64_t max_kv) {
+  static const int forced = [] {
+    const char* env = std::getenv("MI_FA2_DECODE_CHUNK");
+    const int v = env ? std::atoi(env) : 0;
+    return (v >= 128 && v % 128 == 0) ? v : 0;
+  }();
+  if (forced) return forced;
   int chunk = 128;
   while (chunk < (1 << 16) && batch * heads_kv * ((max_kv + chunk - 1) / chunk) > 4096) chunk *= 2;
   return chunk;
@@ -49,11 +58,21 @@ int decode_splits(int64_t max_kv, int chunk) {
   return max_kv > 0 ? (int)((max_kv + chunk - 1) / chunk) : 1;
 }
 
+// Workspace of a split decode: fp32 partial O [B][Hq][splits][128], m [B][Hq][splits] and
+// l [B][Hq][splits].
 size_t decode_workspace(int64_t batch, int64_t heads_q, int64_t heads_kv, int64_t max_kv) {
   const int chunk = decode_chunk(batch, heads_kv, max_kv);
   const int splits = decode_splits(max_kv, chunk);
   if (splits <= 1) return 0;
   return (size_t)batch * heads_q * splits * (mi_fa2::kHeadDim + 2) * sizeof(float);
+}
+
+void set_workspace(FwdParams& p, void* workspace) {
+  float* ws = static_cast<float*>(workspace);
+  const size_t slots = (size_t)p.B * p.Hq * p.max_splits;
+  p.ws_o = ws;
+  p.ws_m = ws + slots * mi_fa2::kHeadDim;
+  p.ws_l = p.ws_m + slots;
 }
 
 int check_common(int32_t dtype, int32_t batch, int32_t heads_q, int32_t heads_kv,
@@ -166,11 +185,7 @@ int mi_fa2_fwd(int32_t dtype, const void* q, const void* k, const void* v, void*
       if (!workspace || workspace_bytes < need)
         return fail(MI_FA2_ERR_WORKSPACE, "decode needs %zu workspace bytes, got %zu", need,
                     workspace ? workspace_bytes : (size_t)0);
-      float* ws = static_cast<float*>(workspace);
-      const size_t slots = (size_t)batch * heads_q * p.max_splits;
-      p.ws_o = ws;
-      p.ws_m = ws + slots * mi_fa2::kHeadDim;
-      p.ws_l = p.ws_m + slots;
+      set_workspace(p, workspace);
     }
     return launched(mi_fa2::launch_decode(p, dtype, mi_fa2::kDense, s));
   }
@@ -278,11 +293,7 @@ int mi_fa2_fwd_paged(int32_t dtype, const void* q, const void* k_pool, const voi
       if (!workspace || workspace_bytes < need)
         return fail(MI_FA2_ERR_WORKSPACE, "decode needs %zu workspace bytes, got %zu", need,
                     workspace ? workspace_bytes : (size_t)0);
-      float* ws = static_cast<float*>(workspace);
-      const size_t slots = (size_t)batch * heads_q * p.max_splits;
-      p.ws_o = ws;
-      p.ws_m = ws + slots * mi_fa2::kHeadDim;
-      p.ws_l = p.ws_m + slots;
+      set_workspace(p, workspace);
     }
     return launched(mi_fa2::launch_decode(p, dtype, mi_fa2::kPaged, s));
   }

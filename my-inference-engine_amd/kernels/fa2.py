@@ -53,8 +53,22 @@ def _envelope(Q, K, V):
     assert K.device == Q.device and V.device == Q.device, "Q, K and V must be on one device"
 
 
+_WORKSPACES = {}
+
+
 def _workspace(nbytes, device):
-    return torch.empty(max(int(nbytes), 0), dtype=torch.uint8, device=device) if nbytes else None
+    """The split-decode workspace of (device, current stream): zero-filled once, grown on demand.
+
+    The kernels leave its counter region at zero when they finish, so it is reused across calls
+    without clearing; one buffer per stream keeps calls on different streams from sharing it."""
+    if not nbytes:
+        return None
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(int(nbytes), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
 
 
 class FlashAttention2Function(torch.autograd.Function):
@@ -94,7 +108,7 @@ class FlashAttention2Function(torch.autograd.Function):
                 batch_size, num_heads, num_kv_heads, seq_len, seq_len_k, d,
                 _strides(q), _strides(k), _strides(v), _strides(O), _strides(L),
                 int(bool(is_causal)), sm_scale,
-                ws.data_ptr() if ws is not None else None, nbytes, _lib.stream_of(Q)))
+                ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _lib.stream_of(Q)))
 
         ctx.save_for_backward(Q, K, V, O, L)
         ctx.is_causal = is_causal
@@ -163,7 +177,7 @@ def fa2_paged(q, k_pool, v_pool, block_table, kv_lens, *, block_size=16, max_kv_
             L.data_ptr(), block_table.data_ptr(), block_table.stride(0), kv_lens.data_ptr(),
             B, Hq, Hkv, T, int(max_kv_len), d, block_size, k_pool.shape[0] // block_size,
             _strides(q), pool_strides, _strides(O), _strides(L), int(bool(is_causal)),
-            1.0 / math.sqrt(d), ws.data_ptr() if ws is not None else None, nbytes,
+            1.0 / math.sqrt(d), ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
             _lib.stream_of(q)))
     return (O, L) if return_lse else O
 
