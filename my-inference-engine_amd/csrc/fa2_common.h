@@ -37,6 +37,14 @@ constexpr float kLog2e = 1.44269504088896340736f;
 enum KvMode { kDense = 0, kVarlen = 1, kPaged = 2 };
 
 struct BF16 {
+  static constexpr uint32_t kOnes2 = 0x3f803f80u;  // (1.0, 1.0)
+  // acc + lo(a) + hi(a): sums two packed values in fp32 (v_dot2c_f32_bf16 against ones)
+  static __device__ __forceinline__ float sum2(uint32_t a, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                           __builtin_bit_cast(bf16x2, kOnes2), acc, false);
+  }
+  static __device__ __forceinline__ float lo(uint32_t a) { return __uint_as_float(a << 16); }
+  static __device__ __forceinline__ float hi(uint32_t a) { return __uint_as_float(a & 0xffff0000u); }
   static __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -53,6 +61,17 @@ struct BF16 {
 };
 
 struct FP16 {
+  static constexpr uint32_t kOnes2 = 0x3c003c00u;  // (1.0, 1.0)
+  static __device__ __forceinline__ float sum2(uint32_t a, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, kOnes2),
+                                  acc, false);
+  }
+  static __device__ __forceinline__ float lo(uint32_t a) {
+    return (float)__builtin_bit_cast(f16x2, a)[0];
+  }
+  static __device__ __forceinline__ float hi(uint32_t a) {
+    return (float)__builtin_bit_cast(f16x2, a)[1];
+  }
   static __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
@@ -101,6 +120,21 @@ struct FwdParams {
 };
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Raw buffer resource over [base, base + bytes): loads at offsets past `bytes` return zeros, which
+// is how the kernels zero-fill keys past a row's end without a branch per load.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 ld16_buf(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+}
+
+// Bytes x.b[s0..] per selector: v_perm_b32 picks bytes of {hi_word, lo_word}.
+__device__ __forceinline__ uint32_t perm_b32(uint32_t hi_word, uint32_t lo_word, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi_word, lo_word, sel);
+}
 
 __device__ __forceinline__ float fmax3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
 

@@ -5,30 +5,54 @@
 // row's keys in tiles, applies the per-row key count and the bottom-right causal mask, and keeps an
 // online softmax (kernels/fa2.py:122-158).  Same mathematics, different organisation:
 //
-//   * One work-group = 4 waves = 128 query rows of one query head; each wave owns 32 rows.
-//   * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16: the accumulator then
-//     holds one query per lane (lane%32) and 16 keys per lane in registers.  That is exactly the
-//     B-operand layout of O^T += V^T P^T, so P never leaves registers, and the running max / sum and
-//     the O rescale are per-lane (one cross-lane exchange with lane^32 per tile for the max).
-//   * Q (the B operand of S^T) lives in registers for the whole key loop.
-//   * A 64-key K tile is kept row-major in LDS (A operand: 16 contiguous bytes per lane); the V tile
-//     is transposed on its way into LDS (V^T rows of 64 keys), so the V^T A operand is two 8-byte
-//     LDS reads.  Row pitches are padded to keep both LDS read patterns bank-conflict free.
-//   * The next tile's global loads are issued before the current tile is computed (register
-//     prefetch), so HBM/L2 latency hides behind the MFMA work.
-//   * Scores are scaled into the exp2 domain once (scale*log2 e folded into one FMA), masking runs
-//     only on tiles that straddle the causal diagonal or the end of the row, and tiles past the
-//     diagonal are never loaded.
-//   * Grid (heads, tiles, batch) with tiles launched longest-first, so causal work drains evenly.
+//   * One work-group = 8 waves = 128 query rows of one query head.  Wave w owns rows 32*(w%4) ..
+//     +31 and key stream w/4: stream 0 takes the even 64-key tiles, stream 1 the odd ones, so two
+//     waves share every SIMD (one's softmax hides behind the other's MFMAs) and the longest causal
+//     tile is walked by two waves in parallel.  The two streams' (m, l, O) are merged in LDS at the
+//     end.
+//   * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16: the accumulator holds
+//     one query per lane (lane%32) and 16 keys per lane in registers.  That is exactly the B-operand
+//     layout of O^T += V^T P^T, so P never leaves registers and the running max / sum and the O
+//     rescale are per lane (one exchange with lane^32 per tile for the max).
+//   * Q lives in registers (the B operand of S^T) for the whole key loop.  Scores stay in the
+//     exp2 domain: p = exp2(s * sm_scale*log2(e) - m) is one FMA and one v_exp per score.  (Folding
+//     the scale into Q would save the FMA but rounds sm_scale*log2(e)*q to 16 bits, which measured
+//     past the 1e-2 output tolerance on short rows.)  The row sum is taken on the packed 16-bit P
+//     with v_dot2 (two scores per instruction).
+//   * The running max is only moved when a row's new max exceeds it by more than 2^8
+//     (kRescaleSlack); until then exp2(s - m) <= 2^8 is exact enough in fp32/bf16 and the O rescale
+//     is skipped wave-wide.
+//   * K tiles are kept row-major in LDS (A operand: 16 contiguous bytes per lane); V tiles are
+//     transposed on their way into LDS (V^T rows of 64 keys, v_perm_b32).  MFMA row m of S^T is
+//     loaded from key pi(m) (a fixed permutation of the 32 keys of a block) so that the 8 keys each
+//     lane holds per 16-key k-step are consecutive: the V^T A operand is then one 16-byte LDS read.
+//     Row pitches (272 B for K, 144 B for V^T) and the staging lane order are chosen so that all
+//     LDS reads and writes of the loop are bank-conflict free on gfx950 (measured).
+//   * Dense and packed K/V are staged with raw buffer loads whose resource ends at the last key
+//     the work-group needs: keys past it read as zeros, with no per-load predicate.
+//   * LDS holds two stages of (K, V^T) for both streams; the next 128 keys are loaded into
+//     registers while the current ones are computed and written to the other stage after, one
+//     barrier per 128 keys.
+//   * Masking runs only on tiles that straddle the causal diagonal or the end of the row, and tiles
+//     past the diagonal are never loaded.  The grid is (heads, tiles, batch) with the longest tiles
+//     launched first so causal work drains evenly.
 #include "fa2_common.h"
 
 namespace mi_fa2 {
 
-constexpr int kPfWaves = 4;
-constexpr int kPfRows = 32 * kPfWaves;  // query rows per work-group
-constexpr int kPfBc = 64;               // keys per K/V tile
-constexpr int kKPitch = kHeadDim + 8;   // LDS row pitch of the K tile, elements (272 B)
-constexpr int kVPitch = kPfBc + 4;      // LDS row pitch of the transposed V tile, elements (136 B)
+constexpr int kPfRowGroups = 4;                  // 32-row query groups per work-group
+constexpr int kPfStreams = 2;                    // key streams per work-group
+constexpr int kPfWaves = kPfRowGroups * kPfStreams;
+constexpr int kPfThreads = 64 * kPfWaves;
+constexpr int kPfRows = 32 * kPfRowGroups;       // query rows per work-group
+constexpr int kPfBc = 64;                        // keys per tile (one stream's share of a step)
+constexpr int kPfStep = kPfBc * kPfStreams;      // keys per step
+constexpr int kKPitch = kHeadDim + 8;            // LDS row pitch of a K tile, elements (272 B)
+constexpr int kVPitch = kPfBc + 8;               // LDS row pitch of a V^T tile, elements (144 B)
+constexpr int kKTile = kPfBc * kKPitch;
+constexpr int kVTile = kHeadDim * kVPitch;
+constexpr int kStage = kPfStreams * (kKTile + kVTile);  // elements per LDS stage
+constexpr float kRescaleSlack = 8.f;             // log2 units the running max may lag the true max
 
 template <int MODE>
 __device__ __forceinline__ const uint16_t* kv_row(const FwdParams& p, const uint16_t* base,
@@ -45,13 +69,14 @@ __device__ __forceinline__ const uint16_t* kv_row(const FwdParams& p, const uint
 }
 
 template <typename E, int MODE>
-__global__ __launch_bounds__(256, 2) void fa2_prefill_kernel(const FwdParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kPfBc * kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[kHeadDim * kVPitch];
+__global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * kStage];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = wave % kPfRowGroups;
+  const int ks = wave / kPfRowGroups;
   const int h = blockIdx.x;
   const int b = blockIdx.z;
   const int hk = h / p.group;
@@ -59,15 +84,15 @@ __global__ __launch_bounds__(256, 2) void fa2_prefill_kernel(const FwdParams p) 
   int T_b, kv_len;
   int64_t q_off, o_off, l_off, k_off, v_off;
   if constexpr (MODE == kVarlen) {
-    const int qs = p.cu_q[b], ks = p.cu_k[b];
+    const int qs = p.cu_q[b], kst = p.cu_k[b];
     T_b = p.cu_q[b + 1] - qs;
-    kv_len = p.cu_k[b + 1] - ks;
+    kv_len = p.cu_k[b + 1] - kst;
     if (kv_len < 0) kv_len = 0;
     q_off = (int64_t)qs * p.q_st + (int64_t)h * p.q_sh;
     o_off = (int64_t)qs * p.o_st + (int64_t)h * p.o_sh;
     l_off = (int64_t)qs * p.l_st + (int64_t)h * p.l_sh;
-    k_off = (int64_t)ks * p.k_st + (int64_t)hk * p.k_sh;
-    v_off = (int64_t)ks * p.v_st + (int64_t)hk * p.v_sh;
+    k_off = (int64_t)kst * p.k_st + (int64_t)hk * p.k_sh;
+    v_off = (int64_t)kst * p.v_st + (int64_t)hk * p.v_sh;
   } else {
     T_b = p.T;
     kv_len = p.kv_lens ? clamp_len(p.kv_lens[b], p.S) : p.S;
@@ -88,10 +113,11 @@ __global__ __launch_bounds__(256, 2) void fa2_prefill_kernel(const FwdParams p) 
   // Keys the work-group needs: up to what its last valid query row sees.
   int kv_hi = kv_len;
   if (p.causal) kv_hi = min(kv_len, min(q0 + kPfRows, T_b) + off);
-  const int n_kv = kv_hi > 0 ? (kv_hi + kPfBc - 1) / kPfBc : 0;
+  if (kv_hi < 0) kv_hi = 0;
+  const int n_steps = (kv_hi + kPfStep - 1) / kPfStep;
 
   // This wave's rows and the key ranges they need.
-  const int wq0 = q0 + wave * 32;
+  const int wq0 = q0 + rg * 32;
   const bool wave_active = wq0 < T_b;
   const int wq_last = min(wq0 + 31, T_b - 1);
   const int wave_hi = p.causal ? min(kv_len, wq_last + off + 1) : kv_len;   // seen by some row
@@ -100,6 +126,7 @@ __global__ __launch_bounds__(256, 2) void fa2_prefill_kernel(const FwdParams p) 
   const int r32 = lane & 31;
   const int g = lane >> 5;
   const int qrow = wq0 + r32;
+  const float c = p.scale_log2;
 
   // Q^T as the B operand: k-step s covers d = s*16 + g*8 + [0, 8).
   u32x4 qb[8];
@@ -115,123 +142,201 @@ __global__ __launch_bounds__(256, 2) void fa2_prefill_kernel(const FwdParams p) 
   f32x16 oacc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) oacc[i] = f32x16{};
-  float m_run = -INFINITY;
-  float l_run = 0.f;
-  const float c = p.scale_log2;
+  float m_run = -INFINITY;  // running max of c*score (log2 units); -inf until a key is seen
+  float l_run = 0.f;        // this lane's partial sum of exp2(c*score - m_run)
   const int lim = p.causal ? min(kv_len, qrow + off + 1) : kv_len;  // keys < lim are visible
 
-  // Staging: thread tid moves K rows st_row + 16u and V rows 4*st_row + r, 16-byte chunk st_dc.
-  const int st_dc = tid & 15;
-  const int st_row = tid >> 4;
+  // Staging of one step (128 keys, both streams).  K: thread tid moves key rows krow + 32u
+  // (u < 4) of the step, 16-byte column chunk kdc.  V: wave w, lane l moves keys 4*(l%16) .. +3 of
+  // stream w%2's tile, dims 8*vdc .. +7, vdc = 4*(w/2) + l/16; lanes walk keys fastest so the
+  // transposed 8-byte writes of a wave land on distinct LDS banks.
+  const int kdc = tid & 15;
+  const int krow = tid >> 4;  // 0..31
+  const int vkg = lane & 15;
+  const int vs = wave & 1;
+  const int vdc = 4 * (wave >> 1) + (lane >> 4);
+  const int vkey = vs * kPfBc + 4 * vkg;  // first of this thread's 4 V keys within the step
   u32x4 kreg[4], vreg[4];
+  // Non-paged modes: byte offsets of this thread's rows relative to the step's first key.
+  const int k_voff = (int)((int64_t)krow * p.k_st + kdc * 8) * 2;
+  const int k_voff32 = (int)(32 * p.k_st) * 2;
+  const int v_voff = (int)((int64_t)vkey * p.v_st + vdc * 8) * 2;
+  const int v_vst = (int)p.v_st * 2;
 
-  auto load_tile = [&](int j) {
-    const int kt = j * kPfBc;
+  auto load_step = [&](int j) {
+    const int kt = j * kPfStep;
+    if constexpr (MODE == kPaged) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int t = kt + krow + 32 * u;
+        const uint16_t* ptr = t < kv_hi ? kv_row<MODE>(p, p.k, k_off, p.k_st, b, t) : nullptr;
+        kreg[u] = ptr ? ld16(ptr + kdc * 8) : u32x4{0, 0, 0, 0};
+      }
+      // the 4 keys share one block: block_size is a multiple of 16 and vkey a multiple of 4
+      const int t0 = kt + vkey;
+      const uint16_t* ptr = t0 < kv_hi ? kv_row<MODE>(p, p.v, v_off, p.v_st, b, t0) : nullptr;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        vreg[r] = (ptr && t0 + r < kv_hi) ? ld16(ptr + (int64_t)r * p.v_st + vdc * 8)
+                                          : u32x4{0, 0, 0, 0};
+    } else {
+      // Resources start at key kt and end at key kv_hi: later keys read as zeros.
+      const int rows = min(kv_hi - kt, kPfStep);
+      const __amdgpu_buffer_rsrc_t kr =
+          make_rsrc(p.k + k_off + (int64_t)kt * p.k_st, (int)(rows * p.k_st * 2));
+      const __amdgpu_buffer_rsrc_t vr =
+          make_rsrc(p.v + v_off + (int64_t)kt * p.v_st, (int)(rows * p.v_st * 2));
+#pragma unroll
+      for (int u = 0; u < 4; ++u) kreg[u] = ld16_buf(kr, k_voff + u * k_voff32);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vreg[r] = ld16_buf(vr, v_voff + r * v_vst);
+    }
+  };
+
+  auto store_step = [&](int stage) {
+    uint16_t* base = smem + stage * kStage;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int t = kt + st_row + 16 * u;
-      const uint16_t* ptr = t < kv_len ? kv_row<MODE>(p, p.k, k_off, p.k_st, b, t) : nullptr;
-      kreg[u] = ptr ? ld16(ptr + st_dc * 8) : u32x4{0, 0, 0, 0};
+      const int row = krow + 32 * u;  // 0..127: stream row / 64, key row % 64
+      *reinterpret_cast<u32x4*>(base + (row >> 6) * kKTile + (row & 63) * kKPitch + kdc * 8) =
+          kreg[u];
     }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = kt + st_row * 4 + r;
-      const uint16_t* ptr = t < kv_len ? kv_row<MODE>(p, p.v, v_off, p.v_st, b, t) : nullptr;
-      vreg[r] = ptr ? ld16(ptr + st_dc * 8) : u32x4{0, 0, 0, 0};
-    }
-  };
-
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      *reinterpret_cast<u32x4*>(k_lds + (st_row + 16 * u) * kKPitch + st_dc * 8) = kreg[u];
     // 4 keys x 8 dims -> 8 dims x 4 keys (V^T rows hold consecutive keys).
+    uint16_t* vt = base + kPfStreams * kKTile + vs * kVTile + 4 * vkg;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const uint32_t a0 = vreg[0][e], a1 = vreg[1][e], a2 = vreg[2][e], a3 = vreg[3][e];
-      const u32x2 lo = {(a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16)};
-      const u32x2 hi = {(a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u)};
-      *reinterpret_cast<u32x2*>(v_lds + (st_dc * 8 + 2 * e) * kVPitch + st_row * 4) = lo;
-      *reinterpret_cast<u32x2*>(v_lds + (st_dc * 8 + 2 * e + 1) * kVPitch + st_row * 4) = hi;
+      const u32x2 lo = {perm_b32(vreg[1][e], vreg[0][e], 0x05040100u),
+                        perm_b32(vreg[3][e], vreg[2][e], 0x05040100u)};
+      const u32x2 hi = {perm_b32(vreg[1][e], vreg[0][e], 0x07060302u),
+                        perm_b32(vreg[3][e], vreg[2][e], 0x07060302u)};
+      *reinterpret_cast<u32x2*>(vt + (vdc * 8 + 2 * e) * kVPitch) = lo;
+      *reinterpret_cast<u32x2*>(vt + (vdc * 8 + 2 * e + 1) * kVPitch) = hi;
     }
   };
 
-  if (n_kv > 0) load_tile(0);
+  if (n_steps > 0) {
+    load_step(0);
+    store_step(0);
+  }
+  // Every path reaches the loop with no vector load in flight: otherwise the wait for the Q
+  // registers would be placed inside the loop, where it also waits for the prefetch loads.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
 
-  for (int j = 0; j < n_kv; ++j) {
-    __syncthreads();  // every wave is done reading tile j-1
-    store_tile();
-    __syncthreads();  // tile j is in LDS
-    if (j + 1 < n_kv) load_tile(j + 1);
+  for (int j = 0; j < n_steps; ++j) {
+    const int stage = j & 1;
+    if (j + 1 < n_steps) load_step(j + 1);
 
-    const int kt = j * kPfBc;
-    if (!wave_active || kt >= wave_hi) continue;
+    const int kt = j * kPfStep + ks * kPfBc;
+    if (wave_active && kt < wave_hi) {
+      const uint16_t* k_lds = smem + stage * kStage + ks * kKTile;
+      const uint16_t* v_lds = smem + stage * kStage + kPfStreams * kKTile + ks * kVTile;
 
-    // S^T[key][query] for keys kt + [0,32) (s0) and kt + [32,64) (s1).
-    f32x16 s0 = f32x16{}, s1 = f32x16{};
-    const uint16_t* kp = k_lds + r32 * kKPitch + g * 8;
+      // S^T for keys kt + [0,32) (s0) and kt + [32,64) (s1); MFMA row m holds key
+      // pi(m) = 16*(m/16) + 8*((m/4)%2) + 4*((m/8)%2) + m%4 of its 32-key block.
+      const int pim = 16 * (r32 >> 4) + 8 * ((r32 >> 2) & 1) + 4 * ((r32 >> 3) & 1) + (r32 & 3);
+      const uint16_t* kp = k_lds + pim * kKPitch + g * 8;
+      f32x16 s0 = f32x16{}, s1 = f32x16{};
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const u32x4 a0 = *reinterpret_cast<const u32x4*>(kp + s * 16);
-      const u32x4 a1 = *reinterpret_cast<const u32x4*>(kp + 32 * kKPitch + s * 16);
-      s0 = E::mfma32(a0, qb[s], s0);
-      s1 = E::mfma32(a1, qb[s], s1);
-    }
+      for (int s = 0; s < 8; ++s) {
+        const u32x4 a0 = *reinterpret_cast<const u32x4*>(kp + s * 16);
+        const u32x4 a1 = *reinterpret_cast<const u32x4*>(kp + 32 * kKPitch + s * 16);
+        s0 = E::mfma32(a0, qb[s], s0);
+        s1 = E::mfma32(a1, qb[s], s1);
+      }
 
-    // Accumulator r of this lane is key kt + 8*(r/4) + 4*g + r%4 (+32 for s1).
-    if (kt + kPfBc > wave_full) {
+      // Accumulator r of this lane is row 8*(r/4) + 4*g + r%4, i.e. key kt + 16*(r/8) + 8*g + r%8
+      // (+32 for s1).
+      if (kt + kPfBc > wave_full) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kt + 16 * (r >> 3) + 8 * g + (r & 7);
+          if (key >= lim) s0[r] = -INFINITY;
+          if (key + 32 >= lim) s1[r] = -INFINITY;
+        }
+      }
+
+      float mx = fmaxf(s0[0], s1[0]);
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmax3(mx, s0[r], s1[r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      // Move the reference max only when the row's max has grown past the slack.
+      const float m_cand = mx * c;
+      const bool grow = m_cand > m_run + kRescaleSlack;
+      if (__any(grow)) {
+        // Lanes that keep their max scale by 1 (never exp2(-inf - -inf) = NaN); a first finite
+        // max scales the empty state by exp2(-inf) = 0.
+        const float alpha = grow ? exp2_fast(m_run - m_cand) : 1.f;
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) oacc[i] *= alpha;
+        if (grow) m_run = m_cand;
+      }
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = kt + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (key >= lim) s0[r] = -INFINITY;
-        if (key + 32 >= lim) s1[r] = -INFINITY;
+        s0[r] = exp2_fast(__builtin_fmaf(s0[r], c, -m_use));
+        s1[r] = exp2_fast(__builtin_fmaf(s1[r], c, -m_use));
+      }
+
+      // P^T as the B operand: k-step kk covers keys kt + 16*kk + 8*g + t in slot t.
+      u32x4 pb[4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        pb[0][w] = E::pack2(s0[2 * w], s0[2 * w + 1]);
+        pb[1][w] = E::pack2(s0[8 + 2 * w], s0[8 + 2 * w + 1]);
+        pb[2][w] = E::pack2(s1[2 * w], s1[2 * w + 1]);
+        pb[3][w] = E::pack2(s1[8 + 2 * w], s1[8 + 2 * w + 1]);
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) l_run = E::sum2(pb[kk][w], l_run);
+
+      // O^T[d][query] += V^T[d][key] P^T[key][query], d-block db covers d = 32*db + lane%32.
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const uint16_t* vp = v_lds + (db * 32 + r32) * kVPitch + g * 8;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+          oacc[db] = E::mfma32(*reinterpret_cast<const u32x4*>(vp + kk * 16), pb[kk], oacc[db]);
       }
     }
 
-    float mx = fmaxf(s0[0], s1[0]);
-#pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmax3(mx, s0[r], s1[r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx * c);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2_fast(m_run - m_use);
-    float ls = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s0[r] = exp2_fast(__builtin_fmaf(s0[r], c, -m_use));
-      s1[r] = exp2_fast(__builtin_fmaf(s1[r], c, -m_use));
-      ls += s0[r] + s1[r];
-    }
-    l_run = l_run * alpha + ls;
-    m_run = m_new;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) oacc[i] *= alpha;
-
-    // P^T as the B operand: k-step ks covers keys kt + 16*ks + 8*(t/4) + 4*g + t%4, slot t.
-    u32x4 pb[4];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      pb[0][w] = E::pack2(s0[2 * w], s0[2 * w + 1]);
-      pb[1][w] = E::pack2(s0[8 + 2 * w], s0[8 + 2 * w + 1]);
-      pb[2][w] = E::pack2(s1[2 * w], s1[2 * w + 1]);
-      pb[3][w] = E::pack2(s1[8 + 2 * w], s1[8 + 2 * w + 1]);
-    }
-
-    // O^T[d][query] += V^T[d][key] P^T[key][query], d-block db covers d = 32*db + lane%32.
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      const uint16_t* vp = v_lds + (db * 32 + r32) * kVPitch + g * 4;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vp + ks * 16);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vp + ks * 16 + 8);
-        const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-        oacc[db] = E::mfma32(a, pb[ks], oacc[db]);
-      }
-    }
+    if (j + 1 < n_steps) store_step(stage ^ 1);
+    __syncthreads();
   }
 
-  if (qrow >= T_b) return;
+  // Merge stream 1 into stream 0 through LDS: [row group][64 O values + m + l][lane].
+  float* red = reinterpret_cast<float*>(smem);
+  constexpr int kRedVals = 66;
+  if (ks == 1) {
+    float* dst = red + rg * kRedVals * 64 + lane;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dst[(db * 16 + r) * 64] = oacc[db][r];
+    dst[64 * 64] = m_run;
+    dst[65 * 64] = l_run;
+  }
+  __syncthreads();
+  if (ks == 1 || qrow >= T_b) return;
+  {
+    const float* src = red + rg * kRedVals * 64 + lane;
+    const float m1 = src[64 * 64];
+    const float l1 = src[65 * 64];
+    const float M = fmaxf(m_run, m1);
+    const float M_use = M == -INFINITY ? 0.f : M;
+    const float f0 = exp2_fast(m_run - M_use);
+    const float f1 = exp2_fast(m1 - M_use);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[db][r] = oacc[db][r] * f0 + src[(db * 16 + r) * 64] * f1;
+    l_run = l_run * f0 + l1 * f1;
+    m_run = M;
+  }
+
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   // Accumulator r of d-block db is d = 32*db + 8*(r/4) + 4*g + r%4: four consecutive d per group.
@@ -239,10 +344,10 @@ __global__ __launch_bounds__(256, 2) void fa2_prefill_kernel(const FwdParams p) 
 #pragma unroll
   for (int db = 0; db < 4; ++db) {
 #pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      const u32x2 val = {E::pack2(oacc[db][rg * 4] * inv, oacc[db][rg * 4 + 1] * inv),
-                         E::pack2(oacc[db][rg * 4 + 2] * inv, oacc[db][rg * 4 + 3] * inv)};
-      *reinterpret_cast<u32x2*>(op + db * 32 + rg * 8) = val;
+    for (int rr = 0; rr < 4; ++rr) {
+      const u32x2 val = {E::pack2(oacc[db][rr * 4] * inv, oacc[db][rr * 4 + 1] * inv),
+                         E::pack2(oacc[db][rr * 4 + 2] * inv, oacc[db][rr * 4 + 3] * inv)};
+      *reinterpret_cast<u32x2*>(op + db * 32 + rr * 8) = val;
     }
   }
   if (p.lse && g == 0)
@@ -255,7 +360,7 @@ static hipError_t launch_prefill_t(const FwdParams& p, int max_seqlen_q, hipStre
   const int n_qt = (max_seqlen_q + kPfRows - 1) / kPfRows;
   if (n_qt == 0 || p.B == 0) return hipSuccess;
   dim3 grid(p.Hq, n_qt, p.B);
-  hipLaunchKernelGGL((fa2_prefill_kernel<E, MODE>), grid, dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((fa2_prefill_kernel<E, MODE>), grid, dim3(kPfThreads), 0, stream, p);
   return hipGetLastError();
 }
 
