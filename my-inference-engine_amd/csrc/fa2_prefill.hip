@@ -146,61 +146,93 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   float l_run = 0.f;        // this lane's partial sum of exp2(c*score - m_run)
   const int lim = p.causal ? min(kv_len, qrow + off + 1) : kv_len;  // keys < lim are visible
 
-  // Staging of one step (128 keys, both streams).  K: thread tid moves key rows krow + 32u
-  // (u < 4) of the step, 16-byte column chunk kdc.  V: wave w, lane l moves keys 4*(l%16) .. +3 of
-  // stream w%2's tile, dims 8*vdc .. +7, vdc = 4*(w/2) + l/16; lanes walk keys fastest so the
-  // transposed 8-byte writes of a wave land on distinct LDS banks.
+  // Software pipeline.  Tile (j, s) is keys 128j + 64s .. +63.  Stream 0 (waves 0-3) works one
+  // tile ahead of stream 1 (waves 4-7) in the score phase, so that in every step one wave of each
+  // SIMD runs its softmax while the other runs MFMAs:
+  //   stream 0, step j: softmax(j, 0) ; PV(j, 0) ; S(j+1, 0)      (VALU, then 32 MFMAs)
+  //   stream 1, step j: PV(j-1, 1) ; S(j, 1) ; softmax(j, 1)      (32 MFMAs, then VALU)
+  // Stage j (LDS slot j%2) therefore holds V(j,0), K(j+1,0), V(j-1,1) and K(j,1); it is loaded
+  // into registers during step j-1 and written to LDS at its end, one barrier per step.
+  //
+  // Staging: K rows krow + 32u: u < 2 is tile K0 (stream 0), u >= 2 tile K1, 16-byte chunk kdc.
+  // V: wave w, lane l moves keys 4*(l%16) .. +3 of tile V(w%2), dims 8*vdc .. +7,
+  // vdc = 4*(w/2) + l/16; lanes walk keys fastest so the transposed 8-byte writes of a wave land
+  // on distinct LDS banks.
   const int kdc = tid & 15;
   const int krow = tid >> 4;  // 0..31
   const int vkg = lane & 15;
   const int vs = wave & 1;
   const int vdc = 4 * (wave >> 1) + (lane >> 4);
-  const int vkey = vs * kPfBc + 4 * vkg;  // first of this thread's 4 V keys within the step
   u32x4 kreg[4], vreg[4];
-  // Non-paged modes: byte offsets of this thread's rows relative to the step's first key.
-  const int k_voff = (int)((int64_t)krow * p.k_st + kdc * 8) * 2;
+  // Non-paged modes: byte offsets of this thread's rows relative to the first key of its tile.
+  const int k_voff = (int)((int64_t)(krow & 31) * p.k_st + kdc * 8) * 2;
   const int k_voff32 = (int)(32 * p.k_st) * 2;
-  const int v_voff = (int)((int64_t)vkey * p.v_st + vdc * 8) * 2;
+  const int v_voff = (int)((int64_t)(4 * vkg) * p.v_st + vdc * 8) * 2;
   const int v_vst = (int)p.v_st * 2;
 
-  auto load_step = [&](int j) {
-    const int kt = j * kPfStep;
+  // Non-paged modes: one resource per tile, starting at its first key and ending at key kv_hi
+  // (or after 64 keys): keys past the end read as zeros.
+  auto tile_rsrc = [&](const uint16_t* base, int64_t st, int start) {
+    const int rows = min(kv_hi - start, kPfBc);
+    if (start < 0 || rows <= 0) return make_rsrc(base, 0);
+    return make_rsrc(base + (int64_t)start * st, (int)(rows * st * 2));
+  };
+
+  // First key of each tile of stage j (may be negative or past kv_hi: then nothing is loaded).
+  auto k0_start = [&](int j) { return (j + 1) * kPfStep; };
+  auto k1_start = [&](int j) { return j * kPfStep + kPfBc; };
+  auto v0_start = [&](int j) { return j * kPfStep; };
+  auto v1_start = [&](int j) { return (j - 1) * kPfStep + kPfBc; };
+
+  // The loads of a stage are issued in two halves (K rows, V rows) at different points of each
+  // stream's program: issued as one burst right after the barrier they back up the CU's memory
+  // pipeline for ~1500 cycles and push the two streams' MFMA phases on top of each other.
+  auto load_stage_k = [&](int j) {
     if constexpr (MODE == kPaged) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int t = kt + krow + 32 * u;
-        const uint16_t* ptr = t < kv_hi ? kv_row<MODE>(p, p.k, k_off, p.k_st, b, t) : nullptr;
+        const int t = (u < 2 ? k0_start(j) : k1_start(j)) + (krow & 31) + 32 * (u & 1);
+        const uint16_t* ptr =
+            (t >= 0 && t < kv_hi) ? kv_row<MODE>(p, p.k, k_off, p.k_st, b, t) : nullptr;
         kreg[u] = ptr ? ld16(ptr + kdc * 8) : u32x4{0, 0, 0, 0};
       }
-      // the 4 keys share one block: block_size is a multiple of 16 and vkey a multiple of 4
-      const int t0 = kt + vkey;
-      const uint16_t* ptr = t0 < kv_hi ? kv_row<MODE>(p, p.v, v_off, p.v_st, b, t0) : nullptr;
+    } else {
+      const __amdgpu_buffer_rsrc_t k0r = tile_rsrc(p.k + k_off, p.k_st, k0_start(j));
+      const __amdgpu_buffer_rsrc_t k1r = tile_rsrc(p.k + k_off, p.k_st, k1_start(j));
+      kreg[0] = ld16_buf(k0r, k_voff);
+      kreg[1] = ld16_buf(k0r, k_voff + k_voff32);
+      kreg[2] = ld16_buf(k1r, k_voff);
+      kreg[3] = ld16_buf(k1r, k_voff + k_voff32);
+    }
+  };
+  auto load_stage_v = [&](int j) {
+    if constexpr (MODE == kPaged) {
+      // the 4 keys share one block: block_size is a multiple of 16 and 4*vkg a multiple of 4
+      const int t0 = (vs ? v1_start(j) : v0_start(j)) + 4 * vkg;
+      const uint16_t* ptr =
+          (t0 >= 0 && t0 < kv_hi) ? kv_row<MODE>(p, p.v, v_off, p.v_st, b, t0) : nullptr;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         vreg[r] = (ptr && t0 + r < kv_hi) ? ld16(ptr + (int64_t)r * p.v_st + vdc * 8)
                                           : u32x4{0, 0, 0, 0};
     } else {
-      // Resources start at key kt and end at key kv_hi: later keys read as zeros.
-      const int rows = min(kv_hi - kt, kPfStep);
-      const __amdgpu_buffer_rsrc_t kr =
-          make_rsrc(p.k + k_off + (int64_t)kt * p.k_st, (int)(rows * p.k_st * 2));
-      const __amdgpu_buffer_rsrc_t vr =
-          make_rsrc(p.v + v_off + (int64_t)kt * p.v_st, (int)(rows * p.v_st * 2));
-#pragma unroll
-      for (int u = 0; u < 4; ++u) kreg[u] = ld16_buf(kr, k_voff + u * k_voff32);
+      const __amdgpu_buffer_rsrc_t vr = vs ? tile_rsrc(p.v + v_off, p.v_st, v1_start(j))
+                                           : tile_rsrc(p.v + v_off, p.v_st, v0_start(j));
 #pragma unroll
       for (int r = 0; r < 4; ++r) vreg[r] = ld16_buf(vr, v_voff + r * v_vst);
     }
   };
+  auto load_stage = [&](int j) {
+    load_stage_k(j);
+    load_stage_v(j);
+  };
 
-  auto store_step = [&](int stage) {
-    uint16_t* base = smem + stage * kStage;
+  auto store_stage = [&](int slot) {
+    uint16_t* base = smem + slot * kStage;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int row = krow + 32 * u;  // 0..127: stream row / 64, key row % 64
-      *reinterpret_cast<u32x4*>(base + (row >> 6) * kKTile + (row & 63) * kKPitch + kdc * 8) =
-          kreg[u];
-    }
+    for (int u = 0; u < 4; ++u)
+      *reinterpret_cast<u32x4*>(base + (u >> 1) * kKTile + ((krow & 31) + 32 * (u & 1)) * kKPitch +
+                                kdc * 8) = kreg[u];
     // 4 keys x 8 dims -> 8 dims x 4 keys (V^T rows hold consecutive keys).
     uint16_t* vt = base + kPfStreams * kKTile + vs * kVTile + 4 * vkg;
 #pragma unroll
@@ -214,96 +246,146 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     }
   };
 
+  // Does this wave compute tile (j, ks)?  Its first key must be one some row of the wave sees.
+  auto tile_kt = [&](int j) { return j * kPfStep + ks * kPfBc; };
+  auto active = [&](int j) { return wave_active && j >= 0 && j < n_steps && tile_kt(j) < wave_hi; };
+
+  // S^T of tile j from the K region of `slot`, MFMA row m holding key
+  // pi(m) = 16*(m/16) + 8*((m/4)%2) + 4*((m/8)%2) + m%4 of its 32-key block; masked to -inf.
+  const int pim = 16 * (r32 >> 4) + 8 * ((r32 >> 2) & 1) + 4 * ((r32 >> 3) & 1) + (r32 & 3);
+  auto scores = [&](int j, int slot, f32x16& s0, f32x16& s1) {
+    const uint16_t* kp = smem + slot * kStage + ks * kKTile + pim * kKPitch + g * 8;
+    s0 = f32x16{};
+    s1 = f32x16{};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(kp + s * 16);
+      const u32x4 a1 = *reinterpret_cast<const u32x4*>(kp + 32 * kKPitch + s * 16);
+      s0 = E::mfma32(a0, qb[s], s0);
+      s1 = E::mfma32(a1, qb[s], s1);
+    }
+
+    // Accumulator r of this lane is row 8*(r/4) + 4*g + r%4, i.e. key kt + 16*(r/8) + 8*g + r%8
+    // (+32 for s1).
+    const int kt = tile_kt(j);
+    if (kt + kPfBc > wave_full) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kt + 16 * (r >> 3) + 8 * g + (r & 7);
+        if (key >= lim) s0[r] = -INFINITY;
+        if (key + 32 >= lim) s1[r] = -INFINITY;
+      }
+    }
+  };
+
+  // Online softmax of one tile's scores: P^T as the B operand (k-step kk covers keys
+  // kt + 16*kk + 8*g + t in slot t), running max / sum / O rescale updated.
+  auto softmax = [&](f32x16& s0, f32x16& s1, u32x4 (&pb)[4]) {
+    float mx = fmaxf(s0[0], s1[0]);
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mx = fmax3(mx, s0[r], s1[r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    // Move the reference max only when the row's max has grown past the slack.
+    const float m_cand = mx * c;
+    const bool grow = m_cand > m_run + kRescaleSlack;
+    if (__any(grow)) {
+      // Lanes that keep their max scale by 1 (never exp2(-inf - -inf) = NaN); a first finite
+      // max scales the empty state by exp2(-inf) = 0.
+      const float alpha = grow ? exp2_fast(m_run - m_cand) : 1.f;
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) oacc[i] *= alpha;
+      if (grow) m_run = m_cand;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s0[r] = exp2_fast(__builtin_fmaf(s0[r], c, -m_use));
+      s1[r] = exp2_fast(__builtin_fmaf(s1[r], c, -m_use));
+    }
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      pb[0][w] = E::pack2(s0[2 * w], s0[2 * w + 1]);
+      pb[1][w] = E::pack2(s0[8 + 2 * w], s0[8 + 2 * w + 1]);
+      pb[2][w] = E::pack2(s1[2 * w], s1[2 * w + 1]);
+      pb[3][w] = E::pack2(s1[8 + 2 * w], s1[8 + 2 * w + 1]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) l_run = E::sum2(pb[kk][w], l_run);
+  };
+
+  // O^T[d][query] += V^T[d][key] P^T[key][query] from the V region of `slot`; d-block db covers
+  // d = 32*db + lane%32.
+  auto pv = [&](int slot, const u32x4 (&pb)[4]) {
+    // k-step outer, d-block inner: four independent accumulators back to back, and the four V^T
+    // reads of a k-step issued together.
+    const uint16_t* vp = smem + slot * kStage + kPfStreams * kKTile + ks * kVTile +
+                         r32 * kVPitch + g * 8;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      u32x4 va[4];
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+        va[db] = *reinterpret_cast<const u32x4*>(vp + db * 32 * kVPitch + kk * 16);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) oacc[db] = E::mfma32(va[db], pb[kk], oacc[db]);
+    }
+
+  };
+
+  // Prologue: stage -1 (slot 1) holds K(0,0) for stream 0's first scores, stage 0 goes to slot 0.
   if (n_steps > 0) {
-    load_step(0);
-    store_step(0);
+    load_stage(-1);
+    store_stage(1);
+    load_stage(0);
+    store_stage(0);
   }
   // Every path reaches the loop with no vector load in flight: otherwise the wait for the Q
   // registers would be placed inside the loop, where it also waits for the prefetch loads.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
-
-  for (int j = 0; j < n_steps; ++j) {
-    const int stage = j & 1;
-    if (j + 1 < n_steps) load_step(j + 1);
-
-    const int kt = j * kPfStep + ks * kPfBc;
-    if (wave_active && kt < wave_hi) {
-      const uint16_t* k_lds = smem + stage * kStage + ks * kKTile;
-      const uint16_t* v_lds = smem + stage * kStage + kPfStreams * kKTile + ks * kVTile;
-
-      // S^T for keys kt + [0,32) (s0) and kt + [32,64) (s1); MFMA row m holds key
-      // pi(m) = 16*(m/16) + 8*((m/4)%2) + 4*((m/8)%2) + m%4 of its 32-key block.
-      const int pim = 16 * (r32 >> 4) + 8 * ((r32 >> 2) & 1) + 4 * ((r32 >> 3) & 1) + (r32 & 3);
-      const uint16_t* kp = k_lds + pim * kKPitch + g * 8;
-      f32x16 s0 = f32x16{}, s1 = f32x16{};
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const u32x4 a0 = *reinterpret_cast<const u32x4*>(kp + s * 16);
-        const u32x4 a1 = *reinterpret_cast<const u32x4*>(kp + 32 * kKPitch + s * 16);
-        s0 = E::mfma32(a0, qb[s], s0);
-        s1 = E::mfma32(a1, qb[s], s1);
+  // The two stream programs run as separate loops (independent register live ranges); both loops
+  // execute the same barriers in the same order, which is all s_barrier needs.
+  if (ks == 0) {
+    f32x16 sa0, sa1;  // scores of the next tile, carried across the barrier
+    if (active(0)) scores(0, 1, sa0, sa1);
+    __syncthreads();  // slot 1 is rewritten at the end of step 0
+    for (int j = 0; j < n_steps; ++j) {
+      const int slot = j & 1;
+      load_stage_k(j + 1);
+      if (active(j)) {
+        u32x4 pb[4];
+        softmax(sa0, sa1, pb);
+        load_stage_v(j + 1);
+        pv(slot, pb);
+      } else {
+        load_stage_v(j + 1);
       }
-
-      // Accumulator r of this lane is row 8*(r/4) + 4*g + r%4, i.e. key kt + 16*(r/8) + 8*g + r%8
-      // (+32 for s1).
-      if (kt + kPfBc > wave_full) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kt + 16 * (r >> 3) + 8 * g + (r & 7);
-          if (key >= lim) s0[r] = -INFINITY;
-          if (key + 32 >= lim) s1[r] = -INFINITY;
-        }
-      }
-
-      float mx = fmaxf(s0[0], s1[0]);
-#pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmax3(mx, s0[r], s1[r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      // Move the reference max only when the row's max has grown past the slack.
-      const float m_cand = mx * c;
-      const bool grow = m_cand > m_run + kRescaleSlack;
-      if (__any(grow)) {
-        // Lanes that keep their max scale by 1 (never exp2(-inf - -inf) = NaN); a first finite
-        // max scales the empty state by exp2(-inf) = 0.
-        const float alpha = grow ? exp2_fast(m_run - m_cand) : 1.f;
-        l_run *= alpha;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) oacc[i] *= alpha;
-        if (grow) m_run = m_cand;
-      }
-      const float m_use = m_run == -INFINITY ? 0.f : m_run;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s0[r] = exp2_fast(__builtin_fmaf(s0[r], c, -m_use));
-        s1[r] = exp2_fast(__builtin_fmaf(s1[r], c, -m_use));
-      }
-
-      // P^T as the B operand: k-step kk covers keys kt + 16*kk + 8*g + t in slot t.
-      u32x4 pb[4];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        pb[0][w] = E::pack2(s0[2 * w], s0[2 * w + 1]);
-        pb[1][w] = E::pack2(s0[8 + 2 * w], s0[8 + 2 * w + 1]);
-        pb[2][w] = E::pack2(s1[2 * w], s1[2 * w + 1]);
-        pb[3][w] = E::pack2(s1[8 + 2 * w], s1[8 + 2 * w + 1]);
-      }
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) l_run = E::sum2(pb[kk][w], l_run);
-
-      // O^T[d][query] += V^T[d][key] P^T[key][query], d-block db covers d = 32*db + lane%32.
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const uint16_t* vp = v_lds + (db * 32 + r32) * kVPitch + g * 8;
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-          oacc[db] = E::mfma32(*reinterpret_cast<const u32x4*>(vp + kk * 16), pb[kk], oacc[db]);
-      }
+      if (active(j + 1)) scores(j + 1, slot, sa0, sa1);
+      store_stage(slot ^ 1);
+      __syncthreads();
     }
-
-    if (j + 1 < n_steps) store_step(stage ^ 1);
+    __syncthreads();  // pairs with stream 1's barrier after its last PV
+  } else {
+    u32x4 pbv[4];  // P of the previous tile, carried across the barrier
+    __syncthreads();
+    for (int j = 0; j < n_steps; ++j) {
+      const int slot = j & 1;
+      load_stage_v(j + 1);
+      if (active(j - 1)) pv(slot, pbv);
+      load_stage_k(j + 1);
+      if (active(j)) {
+        f32x16 s0, s1;
+        scores(j, slot, s0, s1);
+        softmax(s0, s1, pbv);
+      }
+      store_stage(slot ^ 1);
+      __syncthreads();
+    }
+    // The last tile's V is in stage n_steps.
+    if (active(n_steps - 1)) pv(n_steps & 1, pbv);
     __syncthreads();
   }
 

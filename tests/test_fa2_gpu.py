@@ -77,7 +77,10 @@ def test_lse_matches_oracle():
     want = sdpa.lse_ref(q, k, True, lens)
     fin = torch.isfinite(want)
     assert torch.equal(fin, torch.isfinite(lse.cpu()))  # row 2 has queries that see no key
-    assert (lse.cpu()[fin] - want[fin]).abs().max().item() < 1e-3
+    # The prefill kernel sums the bf16-rounded P that its PV product uses, so its l is within the
+    # bf16 unit roundoff 2^-8 of the exact sum: |dLSE| <= log(1 + 2^-8) = 3.9e-3.  The decode
+    # kernel sums in fp32 (checked to 1e-3 below).
+    assert (lse.cpu()[fin] - want[fin]).abs().max().item() < math.log1p(2.0 ** -8) + 1e-4
     check_close(out, sdpa.attention_ref(q, k, v, True, lens), what="lse case output")
     # decode (split-KV + combine) LSE
     announce("[gpu] lse decode")
