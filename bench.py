@@ -1,6 +1,6 @@
 """Benchmark of the MI355X attention hot path; prints one JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary] [--no-e2e]
 
 A "step" is one call of the hot path on one batch of synthetic input, inputs resident in HBM:
 
@@ -9,7 +9,9 @@ A "step" is one call of the hot path on one batch of synthetic input, inputs res
   secondary: paged decode, 64 rows with kv_len ~ U[128, 8192] in 16-token blocks under a permuted
       block table -> HBM GB/s (every visible K/V byte once + q, o, block table, lengths), with
       enough pool copies rotated per step that no step finds its K/V in the 256 MB MALL;
-      ragged packed prefill, 16 sequences with L ~ U[16, 1024] -> TFLOP/s.
+      ragged packed prefill, 16 sequences with L ~ U[16, 1024] -> TFLOP/s;
+      end to end, the Qwen2.5-1.5B architecture (random bf16 weights) serving 16 concurrent chats
+      (prompts U[32, 1000], 64 tokens each) through the scheduler -> generated tok/s.
 
 Timing: W untimed warmup steps, then torch.cuda.synchronize(); a HIP event pair on the stream the
 kernels are launched on brackets exactly K steps; synchronize.  The per-launch duration is the
@@ -99,6 +101,34 @@ def bench_decode(steps, warmup, rotate_bytes=2 << 30):
     return ms, wl.decode_bytes(lens), lens, copies
 
 
+def bench_e2e(n_chats=16, reply_tokens=64, lo=32, hi=1000, seed=0):
+    """End-to-end serving of the Qwen2.5-1.5B architecture (28 layers, hidden 1536, 12q/2kv, head_dim
+    128, SwiGLU 8960, vocab 151936, RoPE theta 1e6, tied embeddings) with random N(0, 0.02) bf16
+    weights: n_chats conversations submitted at once, prompts of U[lo, hi] random token ids, each
+    replying exactly reply_tokens tokens (no EOS) with seeded temperature-1 sampling, paged KV in
+    16-token blocks under a 448 MiB budget (1024 blocks).  tok/s = generated tokens / wall time from
+    the first submit to the last finish (metrics/benchmark_concurrency.py:57-76,166-172)."""
+    import torch
+    from engine import Engine, run_concurrent_chats
+    from kv_cache import KVCache
+    from model import QWEN25_1P5B, Qwen2ForCausalLM
+    cfg = QWEN25_1P5B
+    with torch.device("cuda"):
+        model = Qwen2ForCausalLM(cfg)
+    model.init_random(std=0.02, seed=seed)
+    model = model.to(torch.bfloat16).eval()
+    cache = KVCache(1024, 16, "cuda", torch.bfloat16, cfg.num_layers, cfg.num_kv_heads, cfg.head_dim)
+    kv_mib = cache.buf.numel() * cache.buf.element_size() / 2**20
+    eng = Engine(model, cache, max_reply_tokens=reply_tokens, temperature=1.0, seed=seed)
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(lo, hi + 1, (n_chats,), generator=g).tolist()
+    prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in lens]
+    run_concurrent_chats(eng, prompts[:1], reply_tokens=2)   # warm-up (one chat, two tokens)
+    summary = run_concurrent_chats(eng, prompts, reply_tokens)
+    summary.update(prompt_lens_sum=sum(lens), kv_mib=kv_mib)
+    return summary
+
+
 def cpu_prefill_baseline(seq_len=4096, runs=5):
     import torch
     import workloads as wl
@@ -159,6 +189,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-secondary", action="store_true", help="prefill headline only")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the 16-chat end-to-end run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's hot path runs on a single MI355X "
@@ -223,6 +254,20 @@ def main():
                "roofline": {"bound": "mfma", "achieved": round(rt, 2), "peak": PEAK_BF16_TFLOPS,
                             "unit": "TFLOP/s", "frac": round(rt / PEAK_BF16_TFLOPS, 4)}}
         out["secondary"] = [dec, rag]
+        if not args.no_e2e:
+            e2e = bench_e2e()
+            out["secondary"].append({
+                "metric": "e2e tok/s at 16 chats", "value": round(e2e["tok_per_s"], 1),
+                "unit": "tok/s", "wall_s": round(e2e["wall_s"], 3), "tokens": e2e["tokens"],
+                "ttft_p50_s": round(e2e["ttft_p50"], 4), "ttft_p99_s": round(e2e["ttft_p99"], 4),
+                "tpot_s": round(e2e["tpot"], 5),
+                "workload": f"Qwen2.5-1.5B architecture, random N(0,0.02) bf16 weights; 16 chats, "
+                            f"prompts U[32,1000] random ids (sum {e2e['prompt_lens_sum']}), 64 "
+                            f"tokens each, temperature 1, paged KV 1024 x 16-token blocks "
+                            f"({e2e['kv_mib']:.0f} MiB)",
+                "cpu_baseline": None,
+                "cpu_baseline_note": "not run: the 1.5B model over 16 x ~500-token prompts is "
+                                     "hours of CPU time, beyond the bench's minutes budget"})
     print(json.dumps(out), flush=True)
 
 

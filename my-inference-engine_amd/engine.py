@@ -1,0 +1,228 @@
+"""Continuous-batching scheduler over the paged KV cache (the caller of the attention path).
+
+Restates the reference engine's scheduling semantics (chat.py) as one class instead of module
+globals and a daemon worker thread:
+
+  * a message is admitted only if its conversation's history + prompt + a full reply (+ the
+    trailing separator) fit in free blocks (chat.py:117-125), evicting idle conversations
+    least-recently-used first (chat.py:128-146); one that can never fit is rejected
+    (chat.py:214-225), one that does not fit yet is deferred and retried every tick
+    (chat.py:221-229,236-239);
+  * admission runs one un-chunked prefill over the tokens the cache does not hold yet and samples
+    the first reply token (chat.py:157-185); at most one admission per tick, so decoding jobs are
+    not starved (chat.py:247-253);
+  * every tick then runs ONE batched decode step for all active jobs (chat.py:257-308) and samples
+    every row with a single device sync (chat.py:103-107);
+  * a finished reply keeps its cache (the conversation continues), appends the separator and
+    gives back reserved-but-unused blocks (chat.py:194-211).
+
+Tokenizer, stop sequences, streaming listeners and the web UI are outside the attention path and
+not rebuilt; conversations carry token ids.
+"""
+import time
+from collections import deque
+from dataclasses import dataclass, field
+
+import torch
+
+
+@dataclass
+class Conversation:
+    ids: list = field(default_factory=list)  # full token history
+    seq: object = None                       # cache sequence id, None until admitted / after eviction
+    eos_id: int = -1                         # -1: no token ends a reply (chat.py:323, NO_EOS)
+
+
+@dataclass
+class Job:
+    conv: Conversation
+    new_ids: list
+    max_tokens: int
+    next_token: int = None
+    steps: int = 0
+    generated: list = field(default_factory=list)
+    t_submit: float = 0.0
+    t_first: float = None
+    t_done: float = None
+    rejected: str = None
+
+
+class Engine:
+    def __init__(self, model, cache, *, max_reply_tokens=512, temperature=1.0, sep_ids=(198,),
+                 seed=0):
+        self.model = model
+        self.cache = cache
+        self.max_reply_tokens = max_reply_tokens
+        self.temperature = temperature
+        self.sep_ids = list(sep_ids)   # appended after each reply, like "\n" (chat.py:200)
+        self.device = next(model.parameters()).device
+        self.gen = torch.Generator(device=self.device).manual_seed(seed)
+        self.queue = deque()
+        self.active = []
+        self.deferred = []
+        self.resident = []   # conversations holding cache, least recently used first
+        self.finished = []
+
+    # -- public ---------------------------------------------------------------------------------
+    def submit(self, conv, new_ids, max_tokens=None):
+        job = Job(conv, list(new_ids), max_tokens or self.max_reply_tokens,
+                  t_submit=time.perf_counter())
+        self.queue.append(job)
+        return job
+
+    def release(self, conv):
+        """Free a conversation's blocks now (chat.py:325-330)."""
+        if conv.seq is not None:
+            self._evict(conv)
+
+    def idle(self):
+        return not (self.queue or self.active or self.deferred)
+
+    def tick(self):
+        """One worker iteration (chat.py:232-254)."""
+        for job in list(self.deferred):
+            if self._make_room(job):
+                self.deferred.remove(job)
+                self._admit(job)
+        if not self.active and not self.deferred:
+            if self.queue:  # the reference blocks on its queue here
+                self._try_admit_or_defer(self.queue.popleft())
+        elif not self.active:
+            pass  # deferred jobs wait for blocks to be released (the reference sleeps)
+        elif self.queue:
+            self._try_admit_or_defer(self.queue.popleft())
+        self._process()
+
+    def run_until_idle(self, max_ticks=1_000_000):
+        for _ in range(max_ticks):
+            if self.idle():
+                return
+            if not self.active and self.deferred and not self.queue and not any(
+                    self._fits_after_eviction(j) for j in self.deferred):
+                raise RuntimeError("deferred jobs can never be admitted: nothing else will "
+                                   "release cache blocks")
+            self.tick()
+        raise RuntimeError("scheduler did not drain")
+
+    def _fits_after_eviction(self, job):
+        idle_blocks = sum(len(self.cache._block_tables[c.seq]) for c in self.resident
+                          if c.seq is not None and c is not job.conv)
+        need = self.cache.blocks_needed(job.conv.seq, self._reserve_len(job))
+        return need <= self.cache.free_block_count() + idle_blocks
+
+    # -- scheduling -----------------------------------------------------------------------------
+    def _reserve_len(self, job):
+        return len(job.conv.ids) + len(job.new_ids) + job.max_tokens + len(self.sep_ids)
+
+    def _evict(self, conv):
+        self.cache.free(conv.seq)
+        conv.seq = None
+        if conv in self.resident:
+            self.resident.remove(conv)
+
+    def _make_room(self, job):
+        busy = {id(j.conv) for j in self.active} | {id(job.conv)}
+        while self.cache.blocks_needed(job.conv.seq, self._reserve_len(job)) > self.cache.free_block_count():
+            idle = [c for c in self.resident if id(c) not in busy]
+            if not idle:
+                return False
+            self._evict(idle[0])
+        return True
+
+    def _touch(self, conv):
+        if conv in self.resident:
+            self.resident.remove(conv)
+        self.resident.append(conv)
+
+    def _try_admit_or_defer(self, job):
+        if self.cache.blocks_needed(None, self._reserve_len(job)) > self.cache.num_blocks:
+            job.rejected = "conversation is too long for the KV cache"
+            job.t_done = time.perf_counter()
+            self.finished.append(job)
+        elif self._make_room(job):
+            self._admit(job)
+        else:
+            self.deferred.append(job)
+
+    def _admit(self, job):
+        conv = job.conv
+        reserve = self._reserve_len(job)
+        conv.ids.extend(job.new_ids)
+        if conv.seq is None:
+            conv.seq = self.cache.alloc()
+        prefill = conv.ids[self.cache.length(conv.seq):]
+        self.cache.ensure_capacity(conv.seq, reserve)
+        self._touch(conv)
+        input_ids = torch.tensor([prefill], device=self.device)
+        with torch.no_grad():
+            logits = self.model(input_ids, self.cache, [conv.seq])
+        job.next_token = self._sample(logits[:, -1])[0]
+        job.t_first = time.perf_counter()
+        self.active.append(job)
+
+    def _finish(self, job):
+        conv = job.conv
+        conv.ids.extend(self.sep_ids)
+        self.cache.trim(conv.seq)
+        self._touch(conv)
+        job.t_done = time.perf_counter()
+        self.active.remove(job)
+        self.finished.append(job)
+
+    def _process(self):
+        continuing = []
+        for job in list(self.active):
+            tok = job.next_token
+            job.conv.ids.append(tok)
+            job.generated.append(tok)
+            if tok == job.conv.eos_id:
+                self._finish(job)
+                continue
+            job.steps += 1
+            if job.steps >= job.max_tokens:
+                self._finish(job)
+                continue
+            continuing.append(job)
+        if not continuing:
+            return
+        seqs = [j.conv.seq for j in continuing]
+        input_ids = torch.tensor([[j.next_token] for j in continuing], device=self.device)
+        with torch.no_grad():
+            logits = self.model(input_ids, self.cache, seqs)
+        for job, tok in zip(continuing, self._sample(logits[:, -1])):
+            job.next_token = tok
+
+    def _sample(self, logits):
+        """One id per row of [B, vocab] logits, one device sync for all rows (chat.py:103-107)."""
+        probs = torch.softmax(logits.float() / self.temperature, dim=-1)
+        return torch.multinomial(probs, 1, generator=self.gen).squeeze(1).tolist()
+
+
+def run_concurrent_chats(engine, prompts, reply_tokens):
+    """Start len(prompts) fresh conversations at once and run them to completion.
+
+    Returns the reference benchmark's summary (metrics/benchmark_concurrency.py:57-76): generated
+    tokens / wall time from the first submit to the last finish, TTFT / latency percentiles,
+    time per output token."""
+    convs = [Conversation() for _ in prompts]
+    start = time.perf_counter()
+    jobs = [engine.submit(c, p, reply_tokens) for c, p in zip(convs, prompts)]
+    engine.run_until_idle()
+    torch.cuda.synchronize() if engine.device.type == "cuda" else None
+    wall = time.perf_counter() - start
+    for c in convs:
+        engine.release(c)
+
+    def pct(vals, q):
+        vals = sorted(vals)
+        pos = q / 100 * (len(vals) - 1)
+        lo, hi = int(pos), min(int(pos) + 1, len(vals) - 1)
+        return vals[lo] + (vals[hi] - vals[lo]) * (pos - lo)
+
+    tokens = sum(len(j.generated) for j in jobs)
+    ttft = [j.t_first - j.t_submit for j in jobs]
+    lat = [j.t_done - j.t_submit for j in jobs]
+    tpot = [(j.t_done - j.t_first) / (len(j.generated) - 1) for j in jobs if len(j.generated) > 1]
+    return {"chats": len(prompts), "tokens": tokens, "wall_s": wall, "tok_per_s": tokens / wall,
+            "ttft_p50": pct(ttft, 50), "ttft_p99": pct(ttft, 99), "lat_p50": pct(lat, 50),
+            "lat_p99": pct(lat, 99), "tpot": sum(tpot) / max(1, len(tpot))}

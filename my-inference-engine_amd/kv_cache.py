@@ -1,0 +1,163 @@
+"""Paged KV cache feeding the MI355X paged attention kernels.
+
+Same layout and bookkeeping as the reference's KVCache (kv_cache.py:8-121): one buffer
+[num_layers, 2, num_blocks * block_size, num_kv_heads, head_dim] (dim 1: k=0, v=1), a free list of
+blocks, per-sequence block tables, and logical token p of a sequence at physical slot
+table[p // block_size] * block_size + p % block_size (kv_cache.py:15-16).  The API (alloc, free,
+length, blocks_needed, ensure_capacity, trim, prepare, advance, write, read) keeps the reference's
+names and meaning.
+
+What changes is the per-step metadata.  The reference builds a Python list per new token and a
+dense [B, S] gather index every step (kv_cache.py:74-101), then copies every cached token of every
+row into a dense tensor per layer (kv_cache.py:117-121).  Here prepare() builds, with vectorised
+numpy and ONE pinned host-to-device copy, exactly what the paged kernel reads:
+
+  * block_table [B, W] int32 (rows padded with block 0, kv_cache.py:95),
+  * kv_lens [B] int32 (keys per row after this step, model.py:175),
+  * slot_mapping [B*T] (where this step's new tokens go, for write()),
+
+and no per-layer gather happens on the GPU path.  read() (the dense gather) is kept for the CPU
+fallback and for reference-compatible callers.
+"""
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+
+@dataclass
+class StepMeta:
+    """Metadata of one forward step over rows `seqs`, each appending T tokens."""
+    starts: list                 # tokens each row held before this step (host ints)
+    T: int
+    block_size: int
+    starts_dev: torch.Tensor     # [B] int32
+    kv_lens: torch.Tensor        # [B] int32 = starts + T
+    slot_mapping: torch.Tensor   # [B*T] int64, row-major (row, t)
+    block_table: torch.Tensor    # [B, W] int32
+    tables: list = field(default_factory=list)  # host copies of the rows' block lists
+
+    @property
+    def max_kv(self):
+        return max(self.starts) + self.T
+
+    def gather_idx(self, device):
+        """[B, S] physical slot of every logical position [0, max_kv) (kv_cache.py:93-98)."""
+        S, bs = self.max_kv, self.block_size
+        pos = torch.arange(S, device=device)
+        bt = self.block_table.to(device).long()
+        return bt[:, pos // bs] * bs + pos % bs
+
+    def dense_mask(self, device):
+        """[B, 1, T, S] bottom-right causal mask of the dense fallback (model.py:189-195)."""
+        S = self.max_kv
+        key_pos = torch.arange(S, device=device)
+        starts = torch.tensor(self.starts, device=device)
+        q_pos = starts[:, None] + torch.arange(self.T, device=device)[None, :]
+        return (key_pos[None, None, :] <= q_pos[:, :, None]).unsqueeze(1)
+
+
+class KVCache:
+    def __init__(self, num_blocks, block_size, device, dtype, num_layers, num_kv_heads, head_dim):
+        self.buf = torch.zeros(num_layers, 2, num_blocks * block_size, num_kv_heads, head_dim,
+                               device=device, dtype=dtype)
+        self.num_blocks = num_blocks
+        self.block_size = block_size
+        self.device = torch.device(device)
+        self._free_blocks = list(range(num_blocks))
+        self._block_tables = {}   # seq id -> list of block ids, in logical order
+        self._lengths = {}        # seq id -> tokens written so far
+        self._next_seq = 0
+
+    # -- bookkeeping (kv_cache.py:31-72) -------------------------------------------------------
+    def free_block_count(self):
+        return len(self._free_blocks)
+
+    def blocks_needed(self, seq, total_len):
+        held = len(self._block_tables[seq]) if seq is not None else 0
+        return max(0, math.ceil(total_len / self.block_size) - held)
+
+    def alloc(self):
+        seq = self._next_seq
+        self._next_seq += 1
+        self._block_tables[seq] = []
+        self._lengths[seq] = 0
+        return seq
+
+    def free(self, seq):
+        self._free_blocks.extend(self._block_tables.pop(seq))
+        del self._lengths[seq]
+
+    def length(self, seq):
+        return self._lengths[seq]
+
+    def ensure_capacity(self, seq, total_len):
+        need = self.blocks_needed(seq, total_len)
+        if need > len(self._free_blocks):
+            raise RuntimeError(f"KV cache exhausted: seq {seq} needs {need} more blocks, "
+                               f"only {len(self._free_blocks)} free")
+        table = self._block_tables[seq]
+        for _ in range(need):
+            table.append(self._free_blocks.pop())
+
+    def trim(self, seq):
+        table = self._block_tables[seq]
+        keep = math.ceil(self._lengths[seq] / self.block_size)
+        self._free_blocks.extend(table[keep:])
+        del table[keep:]
+
+    def advance(self, seqs, T):
+        for s in seqs:
+            self._lengths[s] += T
+
+    # -- per-step metadata ----------------------------------------------------------------------
+    def prepare(self, seqs, T):
+        bs = self.block_size
+        starts = [self._lengths[s] for s in seqs]
+        for s, start in zip(seqs, starts):
+            self.ensure_capacity(s, start + T)
+        B = len(seqs)
+        W = max(1, math.ceil((max(starts) + T) / bs))
+        tables = [self._block_tables[s] for s in seqs]
+        # one int32 host array: [starts | kv_lens | block_table B*W | slot_mapping B*T]
+        host = np.zeros(2 * B + B * W + B * T, dtype=np.int32)
+        st = np.asarray(starts, dtype=np.int32)
+        host[:B] = st
+        host[B:2 * B] = st + T
+        bt = host[2 * B:2 * B + B * W].reshape(B, W)
+        for i, t in enumerate(tables):
+            n = min(len(t), W)
+            bt[i, :n] = t[:n]
+        pos = st[:, None] + np.arange(T, dtype=np.int32)[None, :]        # [B, T]
+        rows = np.arange(B)[:, None]
+        host[2 * B + B * W:] = (bt[rows, pos // bs] * bs + pos % bs).reshape(-1)
+        cpu = torch.from_numpy(host)
+        if self.device.type == "cuda":
+            dev = cpu.pin_memory().to(self.device, non_blocking=True)
+        else:
+            dev = cpu.clone()
+        return StepMeta(
+            starts=starts, T=T, block_size=bs,
+            starts_dev=dev[:B], kv_lens=dev[B:2 * B],
+            block_table=dev[2 * B:2 * B + B * W].view(B, W),
+            slot_mapping=dev[2 * B + B * W:].long(),
+            tables=[list(t) for t in tables])
+
+    # -- data movement --------------------------------------------------------------------------
+    def k_pool(self, layer):
+        return self.buf[layer, 0]
+
+    def v_pool(self, layer):
+        return self.buf[layer, 1]
+
+    def write(self, layer, meta, k, v):
+        """Scatter this step's k/v [B, Hkv, T, d] into their slots (kv_cache.py:108-115)."""
+        B, H, T, D = k.shape
+        self.buf[layer, 0].index_copy_(0, meta.slot_mapping, k.transpose(1, 2).reshape(B * T, H, D))
+        self.buf[layer, 1].index_copy_(0, meta.slot_mapping, v.transpose(1, 2).reshape(B * T, H, D))
+
+    def read(self, layer, meta):
+        """Dense [B, Hkv, S, d] copies of every row's keys/values (kv_cache.py:117-121)."""
+        idx = meta.gather_idx(self.buf.device)
+        return (self.buf[layer, 0][idx].transpose(1, 2), self.buf[layer, 1][idx].transpose(1, 2))
