@@ -131,6 +131,52 @@ __device__ __forceinline__ u32x4 ld16_buf(__amdgpu_buffer_rsrc_t r, int byte_off
   return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
 }
 
+// Direct-to-LDS load (gfx950 buffer_load_dwordx4 ... lds): lane l's 16 bytes at byte `voffset` of
+// the raw buffer [base, base + bytes) land at LDS byte address lds_addr + 16*l; offsets past
+// `bytes` write zeros.  base, bytes and lds_addr must be wave-uniform.
+//
+// Issued as inline assembly on purpose: the compiler cannot tell which LDS bytes the intrinsic
+// writes, so it would wait for every such load to finish before the next LDS read of any address
+// (vmcnt(0) in front of the MFMA operand reads of the other stage), serialising the prefetch with
+// the compute it is meant to overlap.  Callers wait with s_waitcnt vmcnt(0) (also as assembly:
+// the compiler drops waits for loads it does not know about) before a barrier.  m0 is written
+// here; the compiler reserves m0 and sets it before every use of its own, so nothing of it is
+// lost.
+__device__ __forceinline__ void lds_dma16(uint64_t base, uint32_t bytes, uint32_t lds_addr,
+                                          int voffset) {
+  const u32x4 rsrc = {(uint32_t)base, (uint32_t)(base >> 32) & 0xffffu, bytes, 0x00020000u};
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"  // one wait state between an SALU write of m0 and an LDS DMA reading it
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(lds_addr), "v"(voffset), "s"(rsrc)
+      : "memory");
+}
+
+// A wave-uniform 64-bit value as such (readfirstlane of both halves; each half is widened as an
+// unsigned 32-bit value, never sign-extended).
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t x) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)x);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(x >> 32));
+  return ((uint64_t)hi << 32) | (uint64_t)lo;
+}
+
+// LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane 4k+q reads 4 16-bit values v[k][4q..4q+3]
+// and lane i receives v[0..3][i] -- a 4x16 transpose.  Used to read V^T operands out of a
+// row-major V tile.
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 ds_read_tr16(const void* lds) {
+  const i16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)const_cast<void*>(lds));
+  return __builtin_bit_cast(u32x2, t);
+}
+
 // Bytes x.b[s0..] per selector: v_perm_b32 picks bytes of {hi_word, lo_word}.
 __device__ __forceinline__ uint32_t perm_b32(uint32_t hi_word, uint32_t lo_word, uint32_t sel) {
   return __builtin_amdgcn_perm(hi_word, lo_word, sel);

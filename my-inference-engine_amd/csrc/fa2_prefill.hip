@@ -22,17 +22,19 @@
 //   * The running max is only moved when a row's new max exceeds it by more than 2^8
 //     (kRescaleSlack); until then exp2(s - m) <= 2^8 is exact enough in fp32/bf16 and the O rescale
 //     is skipped wave-wide.
-//   * K tiles are kept row-major in LDS (A operand: 16 contiguous bytes per lane); V tiles are
-//     transposed on their way into LDS (V^T rows of 64 keys, v_perm_b32).  MFMA row m of S^T is
-//     loaded from key pi(m) (a fixed permutation of the 32 keys of a block) so that the 8 keys each
-//     lane holds per 16-key k-step are consecutive: the V^T A operand is then one 16-byte LDS read.
-//     Row pitches (272 B for K, 144 B for V^T) and the staging lane order are chosen so that all
-//     LDS reads and writes of the loop are bank-conflict free on gfx950 (measured).
-//   * Dense and packed K/V are staged with raw buffer loads whose resource ends at the last key
-//     the work-group needs: keys past it read as zeros, with no per-load predicate.
-//   * LDS holds two stages of (K, V^T) for both streams; the next 128 keys are loaded into
-//     registers while the current ones are computed and written to the other stage after, one
-//     barrier per 128 keys.
+//   * K and V tiles go from memory straight into LDS (buffer_load ... lds: no registers, no LDS
+//     write instructions), row-major, 256 bytes per key, with the 16-byte chunks of each row
+//     XOR-swizzled (K: chunk ^ row%16, V: chunk ^ 4*(row%4)).  The K A operand is one 16-byte read
+//     per lane; the V^T A operand is two ds_read_b64_tr_b16 transposing reads.  MFMA row m of S^T
+//     is loaded from key pi(m) (a fixed permutation of the 32 keys of a block) so that the 8 keys
+//     each lane holds per 16-key k-step are consecutive, which is what the transposing reads
+//     deliver.  The swizzles make every LDS read of the loop bank-conflict free.
+//   * Each load instruction moves 4 key rows (1 KB) through a buffer resource that starts at the
+//     first of them and ends at the last key the work-group needs: keys past it read as zeros,
+//     with no per-lane predicate.  In paged mode the 4 rows always share one block, so the block
+//     table is read once per instruction, by the scalar unit.
+//   * LDS holds two stages of (K, V) for both streams; the next 128 keys are loaded while the
+//     current ones are computed, one barrier per 128 keys.
 //   * Masking runs only on tiles that straddle the causal diagonal or the end of the row, and tiles
 //     past the diagonal are never loaded.  The grid is (heads, tiles, batch) with the longest tiles
 //     launched first so causal work drains evenly.
@@ -47,30 +49,15 @@ constexpr int kPfThreads = 64 * kPfWaves;
 constexpr int kPfRows = 32 * kPfRowGroups;       // query rows per work-group
 constexpr int kPfBc = 64;                        // keys per tile (one stream's share of a step)
 constexpr int kPfStep = kPfBc * kPfStreams;      // keys per step
-constexpr int kKPitch = kHeadDim + 8;            // LDS row pitch of a K tile, elements (272 B)
-constexpr int kVPitch = kPfBc + 8;               // LDS row pitch of a V^T tile, elements (144 B)
-constexpr int kKTile = kPfBc * kKPitch;
-constexpr int kVTile = kHeadDim * kVPitch;
-constexpr int kStage = kPfStreams * (kKTile + kVTile);  // elements per LDS stage
+constexpr int kTileBytes = kPfBc * kHeadDim * 2;       // one 64-key K or V tile in LDS (16 KB)
+constexpr int kStageBytes = kPfStreams * kTileBytes;   // K (or V) tiles of one stage
+constexpr int kVRegion = 2 * kStageBytes;              // V tiles start after both stages' K tiles
+constexpr int kLdsBytes = 2 * kVRegion;                // 128 KB
 constexpr float kRescaleSlack = 8.f;             // log2 units the running max may lag the true max
-
-template <int MODE>
-__device__ __forceinline__ const uint16_t* kv_row(const FwdParams& p, const uint16_t* base,
-                                                  int64_t off, int64_t st, int b, int t) {
-  if constexpr (MODE == kPaged) {
-    const int bs_shift = __builtin_ctz(p.block_size);
-    const int blk = p.block_table[(int64_t)b * p.bt_stride + (t >> bs_shift)];
-    if ((unsigned)blk >= (unsigned)p.num_blocks) return nullptr;
-    const int64_t slot = ((int64_t)blk << bs_shift) + (t & (p.block_size - 1));
-    return base + off + slot * st;
-  } else {
-    return base + off + (int64_t)t * st;
-  }
-}
 
 template <typename E, int MODE>
 __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * kStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -154,28 +141,42 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   // Stage j (LDS slot j%2) therefore holds V(j,0), K(j+1,0), V(j-1,1) and K(j,1); it is loaded
   // into registers during step j-1 and written to LDS at its end, one barrier per step.
   //
-  // Staging: K rows krow + 32u: u < 2 is tile K0 (stream 0), u >= 2 tile K1, 16-byte chunk kdc.
-  // V: wave w, lane l moves keys 4*(l%16) .. +3 of tile V(w%2), dims 8*vdc .. +7,
-  // vdc = 4*(w/2) + l/16; lanes walk keys fastest so the transposed 8-byte writes of a wave land
-  // on distinct LDS banks.
-  const int kdc = tid & 15;
-  const int krow = tid >> 4;  // 0..31
-  const int vkg = lane & 15;
-  const int vs = wave & 1;
-  const int vdc = 4 * (wave >> 1) + (lane >> 4);
-  u32x4 kreg[4], vreg[4];
-  // Non-paged modes: byte offsets of this thread's rows relative to the first key of its tile.
-  const int k_voff = (int)((int64_t)(krow & 31) * p.k_st + kdc * 8) * 2;
-  const int k_voff32 = (int)(32 * p.k_st) * 2;
-  const int v_voff = (int)((int64_t)(4 * vkg) * p.v_st + vdc * 8) * 2;
-  const int v_vst = (int)p.v_st * 2;
+  // Staging.  Every tile is 16 load instructions of 4 rows; wave w issues instructions w and w + 8
+  // of each tile.  Lane l moves row 4i + l/16, LDS chunk l%16, i.e. global chunk
+  // (l%16) ^ swizzle(row); rows 4i and 4(i+8) agree mod 16, so one offset serves both.
+  const int lrow = lane >> 4;
+  const int k_voff = (int)(lrow * p.k_st * 2) + 16 * ((lane & 15) ^ ((4 * wave + lrow) & 15));
+  const int v_voff = (int)(lrow * p.v_st * 2) + 16 * ((lane & 15) ^ (4 * lrow));
 
-  // Non-paged modes: one resource per tile, starting at its first key and ending at key kv_hi
-  // (or after 64 keys): keys past the end read as zeros.
-  auto tile_rsrc = [&](const uint16_t* base, int64_t st, int start) {
-    const int rows = min(kv_hi - start, kPfBc);
-    if (start < 0 || rows <= 0) return make_rsrc(base, 0);
-    return make_rsrc(base + (int64_t)start * st, (int)(rows * st * 2));
+  // One 64-key tile starting at key ts into LDS bytes [lds_off, +16 KB).  Tiles outside
+  // [0, kv_hi) are never read by an active wave and are skipped; rows past kv_hi read as zeros.
+  const uint32_t lds_base = lds_addr_of(smem);
+  auto dma_tile = [&](const uint16_t* base, int64_t off, int64_t st, int ts, int lds_off, int voff) {
+    if (ts < 0 || ts >= kv_hi) return;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i = wave + 8 * h;
+      const int r0 = ts + 4 * i;
+      int n = min(max(kv_hi - r0, 0), 4);
+      const uint16_t* ptr = base;
+      if (n > 0) {
+        if constexpr (MODE == kPaged) {
+          const int bs_shift = __builtin_ctz(p.block_size);
+          const int blk = p.block_table[(int64_t)b * p.bt_stride + (r0 >> bs_shift)];
+          if ((unsigned)blk < (unsigned)p.num_blocks)
+            ptr = base + off + (((int64_t)blk << bs_shift) + (r0 & (p.block_size - 1))) * st;
+          else
+            n = 0;
+        } else {
+          ptr = base + off + (int64_t)r0 * st;
+        }
+      }
+      // The row pointer and length are uniform by construction; say so, or the compiler wraps
+      // the load in a loop over distinct lane values.
+      const uint32_t bytes = __builtin_amdgcn_readfirstlane(n * (int)st * 2);
+      lds_dma16(uniform_u64(reinterpret_cast<uint64_t>(ptr)), bytes,
+                __builtin_amdgcn_readfirstlane(lds_base + lds_off + 1024 * i), voff);
+    }
   };
 
   // First key of each tile of stage j (may be negative or past kv_hi: then nothing is loaded).
@@ -185,65 +186,29 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   auto v1_start = [&](int j) { return (j - 1) * kPfStep + kPfBc; };
 
   // The loads of a stage are issued in two halves (K rows, V rows) at different points of each
-  // stream's program: issued as one burst right after the barrier they back up the CU's memory
-  // pipeline for ~1500 cycles and push the two streams' MFMA phases on top of each other.
+  // stream's program, so the two streams' load bursts do not pile up right after the barrier.
+  // Stage j goes to LDS slot j & 1.
   auto load_stage_k = [&](int j) {
-    if constexpr (MODE == kPaged) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int t = (u < 2 ? k0_start(j) : k1_start(j)) + (krow & 31) + 32 * (u & 1);
-        const uint16_t* ptr =
-            (t >= 0 && t < kv_hi) ? kv_row<MODE>(p, p.k, k_off, p.k_st, b, t) : nullptr;
-        kreg[u] = ptr ? ld16(ptr + kdc * 8) : u32x4{0, 0, 0, 0};
-      }
-    } else {
-      const __amdgpu_buffer_rsrc_t k0r = tile_rsrc(p.k + k_off, p.k_st, k0_start(j));
-      const __amdgpu_buffer_rsrc_t k1r = tile_rsrc(p.k + k_off, p.k_st, k1_start(j));
-      kreg[0] = ld16_buf(k0r, k_voff);
-      kreg[1] = ld16_buf(k0r, k_voff + k_voff32);
-      kreg[2] = ld16_buf(k1r, k_voff);
-      kreg[3] = ld16_buf(k1r, k_voff + k_voff32);
-    }
+    const int o = (j & 1) * kStageBytes;
+    dma_tile(p.k, k_off, p.k_st, k0_start(j), o, k_voff);
+    dma_tile(p.k, k_off, p.k_st, k1_start(j), o + kTileBytes, k_voff);
   };
   auto load_stage_v = [&](int j) {
-    if constexpr (MODE == kPaged) {
-      // the 4 keys share one block: block_size is a multiple of 16 and 4*vkg a multiple of 4
-      const int t0 = (vs ? v1_start(j) : v0_start(j)) + 4 * vkg;
-      const uint16_t* ptr =
-          (t0 >= 0 && t0 < kv_hi) ? kv_row<MODE>(p, p.v, v_off, p.v_st, b, t0) : nullptr;
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        vreg[r] = (ptr && t0 + r < kv_hi) ? ld16(ptr + (int64_t)r * p.v_st + vdc * 8)
-                                          : u32x4{0, 0, 0, 0};
-    } else {
-      const __amdgpu_buffer_rsrc_t vr = vs ? tile_rsrc(p.v + v_off, p.v_st, v1_start(j))
-                                           : tile_rsrc(p.v + v_off, p.v_st, v0_start(j));
-#pragma unroll
-      for (int r = 0; r < 4; ++r) vreg[r] = ld16_buf(vr, v_voff + r * v_vst);
-    }
+    const int o = kVRegion + (j & 1) * kStageBytes;
+    dma_tile(p.v, v_off, p.v_st, v0_start(j), o, v_voff);
+    dma_tile(p.v, v_off, p.v_st, v1_start(j), o + kTileBytes, v_voff);
   };
   auto load_stage = [&](int j) {
     load_stage_k(j);
     load_stage_v(j);
   };
-
-  auto store_stage = [&](int slot) {
-    uint16_t* base = smem + slot * kStage;
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      *reinterpret_cast<u32x4*>(base + (u >> 1) * kKTile + ((krow & 31) + 32 * (u & 1)) * kKPitch +
-                                kdc * 8) = kreg[u];
-    // 4 keys x 8 dims -> 8 dims x 4 keys (V^T rows hold consecutive keys).
-    uint16_t* vt = base + kPfStreams * kKTile + vs * kVTile + 4 * vkg;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const u32x2 lo = {perm_b32(vreg[1][e], vreg[0][e], 0x05040100u),
-                        perm_b32(vreg[3][e], vreg[2][e], 0x05040100u)};
-      const u32x2 hi = {perm_b32(vreg[1][e], vreg[0][e], 0x07060302u),
-                        perm_b32(vreg[3][e], vreg[2][e], 0x07060302u)};
-      *reinterpret_cast<u32x2*>(vt + (vdc * 8 + 2 * e) * kVPitch) = lo;
-      *reinterpret_cast<u32x2*>(vt + (vdc * 8 + 2 * e + 1) * kVPitch) = hi;
-    }
+  // Each wave waits for its own loads, then the barrier publishes them to the work-group.
+  // The builtin wait tells the compiler its own loads (Q) are done; the assembly one is the real
+  // wait for the LDS loads, which the compiler does not track and would drop from the builtin.
+  auto stage_ready = [&]() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
   };
 
   // Does this wave compute tile (j, ks)?  Its first key must be one some row of the wave sees.
@@ -253,14 +218,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   // S^T of tile j from the K region of `slot`, MFMA row m holding key
   // pi(m) = 16*(m/16) + 8*((m/4)%2) + 4*((m/8)%2) + m%4 of its 32-key block; masked to -inf.
   const int pim = 16 * (r32 >> 4) + 8 * ((r32 >> 2) & 1) + 4 * ((r32 >> 3) & 1) + (r32 & 3);
+  // Lane reads row pim (and pim + 32), chunk 2s + g, stored at chunk (2s + g) ^ (pim % 16).
+  const int kx = pim * 256 + 16 * (g ^ (pim & 1)) + 32 * ((pim >> 1) & 7);
   auto scores = [&](int j, int slot, f32x16& s0, f32x16& s1) {
-    const uint16_t* kp = smem + slot * kStage + ks * kKTile + pim * kKPitch + g * 8;
+    const uint8_t* kp = smem + slot * kStageBytes + ks * kTileBytes;
     s0 = f32x16{};
     s1 = f32x16{};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const u32x4 a0 = *reinterpret_cast<const u32x4*>(kp + s * 16);
-      const u32x4 a1 = *reinterpret_cast<const u32x4*>(kp + 32 * kKPitch + s * 16);
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(kp + (kx ^ (32 * s)));
+      const u32x4 a1 = *reinterpret_cast<const u32x4*>(kp + (kx ^ (32 * s)) + 32 * 256);
       s0 = E::mfma32(a0, qb[s], s0);
       s1 = E::mfma32(a1, qb[s], s1);
     }
@@ -318,17 +285,26 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
 
   // O^T[d][query] += V^T[d][key] P^T[key][query] from the V region of `slot`; d-block db covers
   // d = 32*db + lane%32.
+  //
+  // V^T operand of lane l = 16G + 4k + q (g = G/2): d = 32*db + 16*(G%2) + i and keys
+  // 16*kk + 8*g + [0, 8), as two transposing reads of rows 16*kk + 8*g + 4*sec + k, columns
+  // 32*db + 16*(G%2) + 4q .. +3, at swizzled chunk 4*(db ^ k) + 2*(G%2) + q/2.
+  const int vk = (lane >> 2) & 3;
+  const int vx = 2048 * g + 256 * vk + 32 * ((lane >> 4) & 1) + 8 * (lane & 3);
   auto pv = [&](int slot, const u32x4 (&pb)[4]) {
     // k-step outer, d-block inner: four independent accumulators back to back, and the four V^T
     // reads of a k-step issued together.
-    const uint16_t* vp = smem + slot * kStage + kPfStreams * kKTile + ks * kVTile +
-                         r32 * kVPitch + g * 8;
+    const uint8_t* vp = smem + kVRegion + slot * kStageBytes + ks * kTileBytes + vx;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       u32x4 va[4];
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
-        va[db] = *reinterpret_cast<const u32x4*>(vp + db * 32 * kVPitch + kk * 16);
+      for (int db = 0; db < 4; ++db) {
+        const uint8_t* a = vp + 64 * (db ^ vk) + 4096 * kk;
+        const u32x2 lo = ds_read_tr16(a);
+        const u32x2 hi = ds_read_tr16(a + 1024);
+        va[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
 #pragma unroll
       for (int db = 0; db < 4; ++db) oacc[db] = E::mfma32(va[db], pb[kk], oacc[db]);
     }
@@ -338,14 +314,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   // Prologue: stage -1 (slot 1) holds K(0,0) for stream 0's first scores, stage 0 goes to slot 0.
   if (n_steps > 0) {
     load_stage(-1);
-    store_stage(1);
     load_stage(0);
-    store_stage(0);
   }
-  // Every path reaches the loop with no vector load in flight: otherwise the wait for the Q
-  // registers would be placed inside the loop, where it also waits for the prefetch loads.
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  __syncthreads();
+  // Every path reaches the loop with no vector load in flight (the Q registers included).
+  stage_ready();
   // The two stream programs run as separate loops (independent register live ranges); both loops
   // execute the same barriers in the same order, which is all s_barrier needs.
   if (ks == 0) {
@@ -364,8 +336,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
         load_stage_v(j + 1);
       }
       if (active(j + 1)) scores(j + 1, slot, sa0, sa1);
-      store_stage(slot ^ 1);
-      __syncthreads();
+      stage_ready();
     }
     __syncthreads();  // pairs with stream 1's barrier after its last PV
   } else {
@@ -381,8 +352,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
         scores(j, slot, s0, s1);
         softmax(s0, s1, pbv);
       }
-      store_stage(slot ^ 1);
-      __syncthreads();
+      stage_ready();
     }
     // The last tile's V is in stage n_steps.
     if (active(n_steps - 1)) pv(n_steps & 1, pbv);
