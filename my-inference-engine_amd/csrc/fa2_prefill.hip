@@ -36,8 +36,9 @@
 //   * LDS holds two stages of (K, V) for both streams; the next 128 keys are loaded while the
 //     current ones are computed, one barrier per 128 keys.
 //   * Masking runs only on tiles that straddle the causal diagonal or the end of the row, and tiles
-//     past the diagonal are never loaded.  The grid is (heads, tiles, batch) with the longest tiles
-//     launched first so causal work drains evenly.
+//     past the diagonal are never loaded.  The grid is 1-D, mapped XCD-aware: query heads sharing a
+//     kv head run on the same XCDs (one L2 holds their K/V) and every XCD takes its tiles longest
+//     first, so causal work drains evenly.
 #include "fa2_common.h"
 
 namespace mi_fa2 {
@@ -55,8 +56,47 @@ constexpr int kVRegion = 2 * kStageBytes;              // V tiles start after bo
 constexpr int kLdsBytes = 2 * kVRegion;                // 128 KB
 constexpr float kRescaleSlack = 8.f;             // log2 units the running max may lag the true max
 
+// Work-groups are dispatched round-robin over the chip's 8 XCDs (work-group w runs on XCD w % 8),
+// and each XCD has its own L2.  The (row, query head, query tile) of work-group w is chosen so that
+// the query heads sharing one kv head (one class c = (row, kv head)) run on the same XCDs, so an L2
+// holds the K/V of few classes, and so that every XCD walks its tiles longest first with the same
+// mix of causal tile lengths.  rank 0 is a row's last (longest) query tile.
+constexpr int kXcds = 8;
+
+__host__ __device__ inline int prefill_grid_size(int classes, int group, int n_qt) {
+  if (classes < kXcds && kXcds % classes == 0) {
+    const int per_xcd = (classes * group * n_qt + kXcds - 1) / kXcds;
+    return kXcds * per_xcd;
+  }
+  return kXcds * ((classes + kXcds - 1) / kXcds) * group * n_qt;
+}
+
+// Returns false for the padding work-groups of the grid.
+__device__ inline bool prefill_item(int w, int Hkv, int classes, int group, int n_qt, int& b,
+                                    int& h, int& rank) {
+  const int x = w % kXcds, slot = w / kXcds;
+  int c, u;
+  if (classes < kXcds && kXcds % classes == 0) {
+    const int X = kXcds / classes;  // XCDs per class
+    c = x / X;
+    u = slot * X + x % X;
+  } else {
+    const int ncx = (classes - x + kXcds - 1) / kXcds;  // classes x, x + 8, ... live on XCD x
+    if (ncx <= 0) return false;
+    const int per_rank = ncx * group;
+    const int rem = slot % per_rank;
+    c = x + kXcds * (rem / group);
+    u = (slot / per_rank) * group + rem % group;
+  }
+  rank = u / group;
+  if (rank >= n_qt) return false;
+  b = c / Hkv;
+  h = (c % Hkv) * group + u % group;
+  return true;
+}
+
 template <typename E, int MODE>
-__global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdParams p) {
+__global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdParams p, int n_qt_max) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
 
   const int tid = threadIdx.x;
@@ -64,8 +104,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int rg = wave % kPfRowGroups;
   const int ks = wave / kPfRowGroups;
-  const int h = blockIdx.x;
-  const int b = blockIdx.z;
+  int b, h, rank;
+  if (!prefill_item(blockIdx.x, p.Hkv, p.B * p.Hkv, p.group, n_qt_max, b, h, rank)) return;
   const int hk = h / p.group;
 
   int T_b, kv_len;
@@ -90,9 +130,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     v_off = (MODE == kDense ? (int64_t)b * p.v_sb : 0) + (int64_t)hk * p.v_sh;
   }
 
-  // Longest tiles first: blockIdx.y = 0 is the last query tile of the row.
   const int n_qt = (T_b + kPfRows - 1) / kPfRows;
-  const int tile = n_qt - 1 - (int)blockIdx.y;
+  const int tile = n_qt - 1 - rank;
   if (tile < 0) return;
   const int q0 = tile * kPfRows;
   const int off = kv_len - T_b;  // query i sits at key position i + off
@@ -411,8 +450,9 @@ template <typename E, int MODE>
 static hipError_t launch_prefill_t(const FwdParams& p, int max_seqlen_q, hipStream_t stream) {
   const int n_qt = (max_seqlen_q + kPfRows - 1) / kPfRows;
   if (n_qt == 0 || p.B == 0) return hipSuccess;
-  dim3 grid(p.Hq, n_qt, p.B);
-  hipLaunchKernelGGL((fa2_prefill_kernel<E, MODE>), grid, dim3(kPfThreads), 0, stream, p);
+  const int grid = prefill_grid_size(p.B * p.Hkv, p.group, n_qt);
+  hipLaunchKernelGGL((fa2_prefill_kernel<E, MODE>), dim3(grid), dim3(kPfThreads), 0, stream, p,
+                     n_qt);
   return hipGetLastError();
 }
 
