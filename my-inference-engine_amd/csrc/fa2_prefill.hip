@@ -178,43 +178,53 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   //   stream 0, step j: softmax(j, 0) ; PV(j, 0) ; S(j+1, 0)      (VALU, then 32 MFMAs)
   //   stream 1, step j: PV(j-1, 1) ; S(j, 1) ; softmax(j, 1)      (32 MFMAs, then VALU)
   // Stage j (LDS slot j%2) therefore holds V(j,0), K(j+1,0), V(j-1,1) and K(j,1); it is loaded
-  // into registers during step j-1 and written to LDS at its end, one barrier per step.
+  // during step j-1, one barrier per step.
   //
   // Staging.  Every tile is 16 load instructions of 4 rows; wave w issues instructions w and w + 8
   // of each tile.  Lane l moves row 4i + l/16, LDS chunk l%16, i.e. global chunk
   // (l%16) ^ swizzle(row); rows 4i and 4(i+8) agree mod 16, so one offset serves both.
+  // The offsets below are relative to the instruction's first row (paged mode) or to the tile's
+  // first row (the other modes, instruction h adds 32 rows).
   const int lrow = lane >> 4;
-  const int k_voff = (int)(lrow * p.k_st * 2) + 16 * ((lane & 15) ^ ((4 * wave + lrow) & 15));
-  const int v_voff = (int)(lrow * p.v_st * 2) + 16 * ((lane & 15) ^ (4 * lrow));
+  const int trow = MODE == kPaged ? lrow : 4 * wave + lrow;
+  const int k_voff = (int)(trow * p.k_st * 2) + 16 * ((lane & 15) ^ ((4 * wave + lrow) & 15));
+  const int v_voff = (int)(trow * p.v_st * 2) + 16 * ((lane & 15) ^ (4 * lrow));
 
-  // One 64-key tile starting at key ts into LDS bytes [lds_off, +16 KB).  Tiles outside
-  // [0, kv_hi) are never read by an active wave and are skipped; rows past kv_hi read as zeros.
+  // Load instruction h (0, 1) of this wave for the 64-key tile starting at key ts, whose LDS copy
+  // is bytes [lds_off, +16 KB); rows past kv_hi read as zeros.  The scalar work per instruction is
+  // kept small (it competes with the MFMA and softmax instruction streams of the CU's waves):
+  // dense and packed modes use one resource per tile and a per-lane offset per instruction, and
+  // never branch (a tile outside [0, kv_hi) gets a zero-length resource: its loads write zeros that
+  // no active wave reads); paged mode needs one resource per instruction (its 4 rows share a
+  // block, the tile's 64 rows need not) and skips tiles outside [0, kv_hi).
   const uint32_t lds_base = lds_addr_of(smem);
-  auto dma_tile = [&](const uint16_t* base, int64_t off, int64_t st, int ts, int lds_off, int voff) {
-    if (ts < 0 || ts >= kv_hi) return;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int i = wave + 8 * h;
+  auto dma_one = [&](const uint16_t* base, int64_t off, int64_t st, int ts, int lds_off, int voff,
+                     int h) {
+    const int i = wave + 8 * h;
+    const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_base + lds_off + 1024 * i);
+    if constexpr (MODE == kPaged) {
+      if (ts < 0 || ts >= kv_hi) return;
       const int r0 = ts + 4 * i;
       int n = min(max(kv_hi - r0, 0), 4);
       const uint16_t* ptr = base;
       if (n > 0) {
-        if constexpr (MODE == kPaged) {
-          const int bs_shift = __builtin_ctz(p.block_size);
-          const int blk = p.block_table[(int64_t)b * p.bt_stride + (r0 >> bs_shift)];
-          if ((unsigned)blk < (unsigned)p.num_blocks)
-            ptr = base + off + (((int64_t)blk << bs_shift) + (r0 & (p.block_size - 1))) * st;
-          else
-            n = 0;
-        } else {
-          ptr = base + off + (int64_t)r0 * st;
-        }
+        const int bs_shift = __builtin_ctz(p.block_size);
+        const int blk = p.block_table[(int64_t)b * p.bt_stride + (r0 >> bs_shift)];
+        if ((unsigned)blk < (unsigned)p.num_blocks)
+          ptr = base + off + (((int64_t)blk << bs_shift) + (r0 & (p.block_size - 1))) * st;
+        else
+          n = 0;
       }
       // The row pointer and length are uniform by construction; say so, or the compiler wraps
       // the load in a loop over distinct lane values.
-      const uint32_t bytes = __builtin_amdgcn_readfirstlane(n * (int)st * 2);
-      lds_dma16(uniform_u64(reinterpret_cast<uint64_t>(ptr)), bytes,
-                __builtin_amdgcn_readfirstlane(lds_base + lds_off + 1024 * i), voff);
+      lds_dma16(uniform_u64(reinterpret_cast<uint64_t>(ptr)),
+                __builtin_amdgcn_readfirstlane(n * (int)st * 2), lds, voff);
+    } else {
+      const int t0 = max(ts, 0);
+      const int rows = ts < 0 ? 0 : min(max(kv_hi - ts, 0), kPfBc);
+      lds_dma16(uniform_u64(reinterpret_cast<uint64_t>(base + off + (int64_t)t0 * st)),
+                __builtin_amdgcn_readfirstlane(rows * (int)st * 2), lds,
+                voff + h * 32 * (int)st * 2);
     }
   };
 
@@ -224,22 +234,22 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   auto v0_start = [&](int j) { return j * kPfStep; };
   auto v1_start = [&](int j) { return (j - 1) * kPfStep + kPfBc; };
 
-  // The loads of a stage are issued in two halves (K rows, V rows) at different points of each
-  // stream's program, so the two streams' load bursts do not pile up right after the barrier.
-  // Stage j goes to LDS slot j & 1.
-  auto load_stage_k = [&](int j) {
-    const int o = (j & 1) * kStageBytes;
-    dma_tile(p.k, k_off, p.k_st, k0_start(j), o, k_voff);
-    dma_tile(p.k, k_off, p.k_st, k1_start(j), o + kTileBytes, k_voff);
+  // The 8 load instructions of a wave for stage j (which goes to LDS slot j & 1): 4 for K tiles,
+  // 4 for V tiles, q = 2*tile + h.  Inside the key loop they are issued one at a time between the
+  // MFMAs of the score and PV phases rather than as a burst.
+  auto dma_k = [&](int j, int q) {
+    const int o = (j & 1) * kStageBytes + (q >> 1) * kTileBytes;
+    dma_one(p.k, k_off, p.k_st, (q >> 1) ? k1_start(j) : k0_start(j), o, k_voff, q & 1);
   };
-  auto load_stage_v = [&](int j) {
-    const int o = kVRegion + (j & 1) * kStageBytes;
-    dma_tile(p.v, v_off, p.v_st, v0_start(j), o, v_voff);
-    dma_tile(p.v, v_off, p.v_st, v1_start(j), o + kTileBytes, v_voff);
+  auto dma_v = [&](int j, int q) {
+    const int o = kVRegion + (j & 1) * kStageBytes + (q >> 1) * kTileBytes;
+    dma_one(p.v, v_off, p.v_st, (q >> 1) ? v1_start(j) : v0_start(j), o, v_voff, q & 1);
   };
   auto load_stage = [&](int j) {
-    load_stage_k(j);
-    load_stage_v(j);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dma_k(j, q);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dma_v(j, q);
   };
   // Each wave waits for its own loads, then the barrier publishes them to the work-group.
   // The builtin wait tells the compiler its own loads (Q) are done; the assembly one is the real
@@ -259,7 +269,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   const int pim = 16 * (r32 >> 4) + 8 * ((r32 >> 2) & 1) + 4 * ((r32 >> 3) & 1) + (r32 & 3);
   // Lane reads row pim (and pim + 32), chunk 2s + g, stored at chunk (2s + g) ^ (pim % 16).
   const int kx = pim * 256 + 16 * (g ^ (pim & 1)) + 32 * ((pim >> 1) & 7);
-  auto scores = [&](int j, int slot, f32x16& s0, f32x16& s1) {
+  // dma(q), q = 0..3, is called between the MFMAs (the K loads of the next stage).
+  auto scores = [&](int j, int slot, f32x16& s0, f32x16& s1, auto&& dma) {
     const uint8_t* kp = smem + slot * kStageBytes + ks * kTileBytes;
     s0 = f32x16{};
     s1 = f32x16{};
@@ -269,6 +280,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
       const u32x4 a1 = *reinterpret_cast<const u32x4*>(kp + (kx ^ (32 * s)) + 32 * 256);
       s0 = E::mfma32(a0, qb[s], s0);
       s1 = E::mfma32(a1, qb[s], s1);
+      if (s & 1) dma(s >> 1);
     }
 
     // Accumulator r of this lane is row 8*(r/4) + 4*g + r%4, i.e. key kt + 16*(r/8) + 8*g + r%8
@@ -330,7 +342,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   // 32*db + 16*(G%2) + 4q .. +3, at swizzled chunk 4*(db ^ k) + 2*(G%2) + q/2.
   const int vk = (lane >> 2) & 3;
   const int vx = 2048 * g + 256 * vk + 32 * ((lane >> 4) & 1) + 8 * (lane & 3);
-  auto pv = [&](int slot, const u32x4 (&pb)[4]) {
+  // dma(kk), kk = 0..3, is called between the MFMAs (the V loads of the next stage).
+  auto pv = [&](int slot, const u32x4 (&pb)[4], auto&& dma) {
     // k-step outer, d-block inner: four independent accumulators back to back, and the four V^T
     // reads of a k-step issued together.
     const uint8_t* vp = smem + kVRegion + slot * kStageBytes + ks * kTileBytes + vx;
@@ -346,6 +359,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
       }
 #pragma unroll
       for (int db = 0; db < 4; ++db) oacc[db] = E::mfma32(va[db], pb[kk], oacc[db]);
+      dma(kk);
     }
 
   };
@@ -359,22 +373,29 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   stage_ready();
   // The two stream programs run as separate loops (independent register live ranges); both loops
   // execute the same barriers in the same order, which is all s_barrier needs.
+  auto no_dma = [](int) {};
   if (ks == 0) {
     f32x16 sa0, sa1;  // scores of the next tile, carried across the barrier
-    if (active(0)) scores(0, 1, sa0, sa1);
-    __syncthreads();  // slot 1 is rewritten at the end of step 0
+    if (active(0)) scores(0, 1, sa0, sa1, no_dma);
+    __syncthreads();  // slot 1 is rewritten during step 0
     for (int j = 0; j < n_steps; ++j) {
       const int slot = j & 1;
-      load_stage_k(j + 1);
+      auto next_v = [&](int q) { dma_v(j + 1, q); };
+      auto next_k = [&](int q) { dma_k(j + 1, q); };
       if (active(j)) {
         u32x4 pb[4];
         softmax(sa0, sa1, pb);
-        load_stage_v(j + 1);
-        pv(slot, pb);
+        pv(slot, pb, next_v);
       } else {
-        load_stage_v(j + 1);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) next_v(q);
       }
-      if (active(j + 1)) scores(j + 1, slot, sa0, sa1);
+      if (active(j + 1)) {
+        scores(j + 1, slot, sa0, sa1, next_k);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) next_k(q);
+      }
       stage_ready();
     }
     __syncthreads();  // pairs with stream 1's barrier after its last PV
@@ -383,18 +404,26 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     __syncthreads();
     for (int j = 0; j < n_steps; ++j) {
       const int slot = j & 1;
-      load_stage_v(j + 1);
-      if (active(j - 1)) pv(slot, pbv);
-      load_stage_k(j + 1);
+      auto next_v = [&](int q) { dma_v(j + 1, q); };
+      auto next_k = [&](int q) { dma_k(j + 1, q); };
+      if (active(j - 1)) {
+        pv(slot, pbv, next_v);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) next_v(q);
+      }
       if (active(j)) {
         f32x16 s0, s1;
-        scores(j, slot, s0, s1);
+        scores(j, slot, s0, s1, next_k);
         softmax(s0, s1, pbv);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) next_k(q);
       }
       stage_ready();
     }
     // The last tile's V is in stage n_steps.
-    if (active(n_steps - 1)) pv(n_steps & 1, pbv);
+    if (active(n_steps - 1)) pv(n_steps & 1, pbv, no_dma);
     __syncthreads();
   }
 
