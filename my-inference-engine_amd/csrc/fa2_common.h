@@ -182,6 +182,14 @@ __device__ __forceinline__ uint32_t perm_b32(uint32_t hi_word, uint32_t lo_word,
   return __builtin_amdgcn_perm(hi_word, lo_word, sel);
 }
 
+// clamp(x, lo, hi) of a wave-uniform value on the scalar unit (the compiler's clamp pattern is a
+// vector instruction, which then needs a readfirstlane back).
+__device__ __forceinline__ int sclamp(int x, int lo, int hi) {
+  int r;
+  asm("s_max_i32 %0, %1, %2\n\ts_min_i32 %0, %0, %3" : "=&s"(r) : "s"(x), "s"(lo), "s"(hi));
+  return r;
+}
+
 __device__ __forceinline__ float fmax3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }

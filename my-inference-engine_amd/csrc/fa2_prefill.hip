@@ -56,6 +56,11 @@ constexpr int kVRegion = 2 * kStageBytes;              // V tiles start after bo
 constexpr int kLdsBytes = 2 * kVRegion;                // 128 KB
 constexpr float kRescaleSlack = 8.f;             // log2 units the running max may lag the true max
 
+template <int P>
+struct Parity {
+  static constexpr int value = P;
+};
+
 // Work-groups are dispatched round-robin over the chip's 8 XCDs (work-group w runs on XCD w % 8),
 // and each XCD has its own L2.  The (row, query head, query tile) of work-group w is chosen so that
 // the query heads sharing one kv head (one class c = (row, kv head)) run on the same XCDs, so an L2
@@ -221,7 +226,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
                 __builtin_amdgcn_readfirstlane(n * (int)st * 2), lds, voff);
     } else {
       const int t0 = max(ts, 0);
-      const int rows = ts < 0 ? 0 : min(max(kv_hi - ts, 0), kPfBc);
+      const int rows = ts < 0 ? 0 : sclamp(kv_hi - ts, 0, kPfBc);
       lds_dma16(uniform_u64(reinterpret_cast<uint64_t>(base + off + (int64_t)t0 * st)),
                 __builtin_amdgcn_readfirstlane(rows * (int)st * 2), lds,
                 voff + h * 32 * (int)st * 2);
@@ -238,7 +243,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   // 4 for V tiles, q = 2*tile + h.  Inside the key loop they are issued one at a time between the
   // MFMAs of the score and PV phases rather than as a burst.
   auto dma_k = [&](int j, int q) {
-    const int o = (j & 1) * kStageBytes + (q >> 1) * kTileBytes;
+    const int o = (j & 1) * kStageBytes + (q >> 1) * kTileBytes;  // j & 1 folds when j's parity is known
     dma_one(p.k, k_off, p.k_st, (q >> 1) ? k1_start(j) : k0_start(j), o, k_voff, q & 1);
   };
   auto dma_v = [&](int j, int q) {
@@ -378,10 +383,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     f32x16 sa0, sa1;  // scores of the next tile, carried across the barrier
     if (active(0)) scores(0, 1, sa0, sa1, no_dma);
     __syncthreads();  // slot 1 is rewritten during step 0
-    for (int j = 0; j < n_steps; ++j) {
-      const int slot = j & 1;
-      auto next_v = [&](int q) { dma_v(j + 1, q); };
-      auto next_k = [&](int q) { dma_k(j + 1, q); };
+    // One step; `par` is j's parity as a compile-time constant, which turns every LDS offset of
+    // the step into an immediate (the loop below is unrolled by two for that).
+    auto step = [&](int j, auto par) {
+      constexpr int slot = decltype(par)::value;
+      auto next_v = [&](int q) { dma_v(2 * (j >> 1) + slot + 1, q); };
+      auto next_k = [&](int q) { dma_k(2 * (j >> 1) + slot + 1, q); };
       if (active(j)) {
         u32x4 pb[4];
         softmax(sa0, sa1, pb);
@@ -397,15 +404,21 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
         for (int q = 0; q < 4; ++q) next_k(q);
       }
       stage_ready();
+    };
+    int j = 0;
+    for (; j + 2 <= n_steps; j += 2) {
+      step(j, Parity<0>{});
+      step(j + 1, Parity<1>{});
     }
+    if (j < n_steps) step(j, Parity<0>{});
     __syncthreads();  // pairs with stream 1's barrier after its last PV
   } else {
     u32x4 pbv[4];  // P of the previous tile, carried across the barrier
     __syncthreads();
-    for (int j = 0; j < n_steps; ++j) {
-      const int slot = j & 1;
-      auto next_v = [&](int q) { dma_v(j + 1, q); };
-      auto next_k = [&](int q) { dma_k(j + 1, q); };
+    auto step = [&](int j, auto par) {
+      constexpr int slot = decltype(par)::value;
+      auto next_v = [&](int q) { dma_v(2 * (j >> 1) + slot + 1, q); };
+      auto next_k = [&](int q) { dma_k(2 * (j >> 1) + slot + 1, q); };
       if (active(j - 1)) {
         pv(slot, pbv, next_v);
       } else {
@@ -421,7 +434,13 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
         for (int q = 0; q < 4; ++q) next_k(q);
       }
       stage_ready();
+    };
+    int j = 0;
+    for (; j + 2 <= n_steps; j += 2) {
+      step(j, Parity<0>{});
+      step(j + 1, Parity<1>{});
     }
+    if (j < n_steps) step(j, Parity<0>{});
     // The last tile's V is in stage n_steps.
     if (active(n_steps - 1)) pv(n_steps & 1, pbv, no_dma);
     __syncthreads();
