@@ -184,9 +184,13 @@ __device__ __forceinline__ uint32_t perm_b32(uint32_t hi_word, uint32_t lo_word,
 
 // clamp(x, lo, hi) of a wave-uniform value on the scalar unit (the compiler's clamp pattern is a
 // vector instruction, which then needs a readfirstlane back).
+// x must be wave-uniform; it is passed through readfirstlane so that the operand is an SGPR even
+// where the compiler cannot prove the uniformity itself.
 __device__ __forceinline__ int sclamp(int x, int lo, int hi) {
   int r;
-  asm("s_max_i32 %0, %1, %2\n\ts_min_i32 %0, %0, %3" : "=&s"(r) : "s"(x), "s"(lo), "s"(hi));
+  asm("s_max_i32 %0, %1, %2\n\ts_min_i32 %0, %0, %3"
+      : "=&s"(r)
+      : "s"(__builtin_amdgcn_readfirstlane(x)), "s"(lo), "s"(hi));
   return r;
 }
 

@@ -277,14 +277,22 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   // dma(q), q = 0..3, is called between the MFMAs (the K loads of the next stage).
   auto scores = [&](int j, int slot, f32x16& s0, f32x16& s1, auto&& dma) {
     const uint8_t* kp = smem + slot * kStageBytes + ks * kTileBytes;
+    // K operands are read two k-steps ahead of their MFMAs: in this phase the SIMD's other wave
+    // is in its softmax, so nothing else would cover the LDS latency.
+    auto rd = [&](int s, u32x4& a0, u32x4& a1) {
+      a0 = *reinterpret_cast<const u32x4*>(kp + (kx ^ (32 * s)));
+      a1 = *reinterpret_cast<const u32x4*>(kp + (kx ^ (32 * s)) + 32 * 256);
+    };
+    u32x4 ka[3][2];
+    rd(0, ka[0][0], ka[0][1]);
+    rd(1, ka[1][0], ka[1][1]);
     s0 = f32x16{};
     s1 = f32x16{};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const u32x4 a0 = *reinterpret_cast<const u32x4*>(kp + (kx ^ (32 * s)));
-      const u32x4 a1 = *reinterpret_cast<const u32x4*>(kp + (kx ^ (32 * s)) + 32 * 256);
-      s0 = E::mfma32(a0, qb[s], s0);
-      s1 = E::mfma32(a1, qb[s], s1);
+      if (s + 2 < 8) rd(s + 2, ka[(s + 2) % 3][0], ka[(s + 2) % 3][1]);
+      s0 = E::mfma32(ka[s % 3][0], qb[s], s0);
+      s1 = E::mfma32(ka[s % 3][1], qb[s], s1);
       if (s & 1) dma(s >> 1);
     }
 
@@ -352,9 +360,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     // k-step outer, d-block inner: four independent accumulators back to back, and the four V^T
     // reads of a k-step issued together.
     const uint8_t* vp = smem + kVRegion + slot * kStageBytes + ks * kTileBytes + vx;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      u32x4 va[4];
+    // The V^T operands of k-step kk + 1 are read while the MFMAs of k-step kk run.
+    auto rd = [&](int kk, u32x4 (&va)[4]) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         const uint8_t* a = vp + 64 * (db ^ vk) + 4096 * kk;
@@ -362,8 +369,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
         const u32x2 hi = ds_read_tr16(a + 1024);
         va[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
+    };
+    u32x4 va[2][4];
+    rd(0, va[0]);
 #pragma unroll
-      for (int db = 0; db < 4; ++db) oacc[db] = E::mfma32(va[db], pb[kk], oacc[db]);
+    for (int kk = 0; kk < 4; ++kk) {
+      if (kk + 1 < 4) rd(kk + 1, va[(kk + 1) & 1]);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) oacc[db] = E::mfma32(va[kk & 1][db], pb[kk], oacc[db]);
       dma(kk);
     }
 
