@@ -55,6 +55,7 @@ constexpr int kStageBytes = kPfStreams * kTileBytes;   // K (or V) tiles of one 
 constexpr int kVRegion = 2 * kStageBytes;              // V tiles start after both stages' K tiles
 constexpr int kLdsBytes = 2 * kVRegion;                // 128 KB
 constexpr float kRescaleSlack = 8.f;             // log2 units the running max may lag the true max
+constexpr float kSumLimit = 256.f;               // 2^kRescaleSlack
 
 template <int P>
 struct Parity {
@@ -270,7 +271,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   auto active = [&](int j) { return wave_active && j >= 0 && j < n_steps && tile_kt(j) < wave_hi; };
 
   // S^T of tile j from the K region of `slot`, MFMA row m holding key
-  // pi(m) = 16*(m/16) + 8*((m/4)%2) + 4*((m/8)%2) + m%4 of its 32-key block; masked to -inf.
+  // pi(m) = 16*(m/16) + 8*((m/4)%2) + 4*((m/8)%2) + m%4 of its 32-key block (unmasked).
   const int pim = 16 * (r32 >> 4) + 8 * ((r32 >> 2) & 1) + 4 * ((r32 >> 3) & 1) + (r32 & 3);
   // Lane reads row pim (and pim + 32), chunk 2s + g, stored at chunk (2s + g) ^ (pim % 16).
   const int kx = pim * 256 + 16 * (g ^ (pim & 1)) + 32 * ((pim >> 1) & 7);
@@ -295,9 +296,62 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
       s1 = E::mfma32(ka[s % 3][1], qb[s], s1);
       if (s & 1) dma(s >> 1);
     }
+  };
 
-    // Accumulator r of this lane is row 8*(r/4) + 4*g + r%4, i.e. key kt + 16*(r/8) + 8*g + r%8
-    // (+32 for s1).
+  // Online softmax of tile j's scores: P^T as the B operand (k-step kk covers keys
+  // kt + 16*kk + 8*g + t in slot t), running max / sum / O rescale updated.
+  //
+  // Accumulator r of s0 holds key kt + 16*(r/8) + 8*g + r%8 (+32 for s1).  Tiles that straddle the
+  // causal diagonal or the row's end are masked first (keys >= lim to -inf, in registers, inside
+  // the branch), so the common unmasked path runs no mask instructions.
+  //
+  // Fast path: the running max m_run stays the exponent reference and the row max is not
+  // computed.  The reference may lag the true max by kRescaleSlack (every p <= 2^8); a lane whose
+  // 32 values of p sum to at most 2^8 certainly has no p above that, so the max is only looked at
+  // (and the state rescaled) when some lane's sum exceeds it -- or is inf / NaN, which is how the
+  // first tile of a row (m_run = -inf) takes the slow path.  Both paths give the same p whenever
+  // the slow path would not have moved the reference.
+  auto softmax_body = [&](f32x16& s0, f32x16& s1, u32x4 (&pb)[4]) {
+    auto exp_pack_sum = [&](float m_use) {
+      // Pair by pair (exp, pack, sum) so that no more than a pair of fp32 p values is live.
+      float lt = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {  // s0 pairs 2i, 2i+1 -> pb[i/4][i%4]
+        pb[i >> 2][i & 3] = E::pack2(exp2_fast(__builtin_fmaf(s0[2 * i], c, -m_use)),
+                                     exp2_fast(__builtin_fmaf(s0[2 * i + 1], c, -m_use)));
+        lt = E::sum2(pb[i >> 2][i & 3], lt);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {  // s1 pairs -> pb[2 + i/4][i%4]
+        pb[2 + (i >> 2)][i & 3] = E::pack2(exp2_fast(__builtin_fmaf(s1[2 * i], c, -m_use)),
+                                           exp2_fast(__builtin_fmaf(s1[2 * i + 1], c, -m_use)));
+        lt = E::sum2(pb[2 + (i >> 2)][i & 3], lt);
+      }
+      return lt;
+    };
+    float lt = exp_pack_sum(m_run);
+    if (__any(!(lt <= kSumLimit))) {
+      float mx = fmaxf(s0[0], s1[0]);
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmax3(mx, s0[r], s1[r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      // Move the reference max only when the row's max has grown past the slack.
+      const float m_cand = mx * c;
+      const bool grow = m_cand > m_run + kRescaleSlack;
+      if (__any(grow)) {
+        // Lanes that keep their max scale by 1 (never exp2(-inf - -inf) = NaN); a first finite
+        // max scales the empty state by exp2(-inf) = 0.
+        const float alpha = grow ? exp2_fast(m_run - m_cand) : 1.f;
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) oacc[i] *= alpha;
+        if (grow) m_run = m_cand;
+      }
+      lt = exp_pack_sum(m_run == -INFINITY ? 0.f : m_run);
+    }
+    l_run += lt;
+  };
+  auto softmax = [&](int j, f32x16& s0, f32x16& s1, u32x4 (&pb)[4]) {
     const int kt = tile_kt(j);
     if (kt + kPfBc > wave_full) {
 #pragma unroll
@@ -307,44 +361,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
         if (key + 32 >= lim) s1[r] = -INFINITY;
       }
     }
-  };
-
-  // Online softmax of one tile's scores: P^T as the B operand (k-step kk covers keys
-  // kt + 16*kk + 8*g + t in slot t), running max / sum / O rescale updated.
-  auto softmax = [&](f32x16& s0, f32x16& s1, u32x4 (&pb)[4]) {
-    float mx = fmaxf(s0[0], s1[0]);
-#pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmax3(mx, s0[r], s1[r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    // Move the reference max only when the row's max has grown past the slack.
-    const float m_cand = mx * c;
-    const bool grow = m_cand > m_run + kRescaleSlack;
-    if (__any(grow)) {
-      // Lanes that keep their max scale by 1 (never exp2(-inf - -inf) = NaN); a first finite
-      // max scales the empty state by exp2(-inf) = 0.
-      const float alpha = grow ? exp2_fast(m_run - m_cand) : 1.f;
-      l_run *= alpha;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) oacc[i] *= alpha;
-      if (grow) m_run = m_cand;
-    }
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s0[r] = exp2_fast(__builtin_fmaf(s0[r], c, -m_use));
-      s1[r] = exp2_fast(__builtin_fmaf(s1[r], c, -m_use));
-    }
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      pb[0][w] = E::pack2(s0[2 * w], s0[2 * w + 1]);
-      pb[1][w] = E::pack2(s0[8 + 2 * w], s0[8 + 2 * w + 1]);
-      pb[2][w] = E::pack2(s1[2 * w], s1[2 * w + 1]);
-      pb[3][w] = E::pack2(s1[8 + 2 * w], s1[8 + 2 * w + 1]);
-    }
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) l_run = E::sum2(pb[kk][w], l_run);
+    softmax_body(s0, s1, pb);
   };
 
   // O^T[d][query] += V^T[d][key] P^T[key][query] from the V region of `slot`; d-block db covers
@@ -404,7 +421,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
       auto next_k = [&](int q) { dma_k(2 * (j >> 1) + slot + 1, q); };
       if (active(j)) {
         u32x4 pb[4];
-        softmax(sa0, sa1, pb);
+        softmax(j, sa0, sa1, pb);
         pv(slot, pb, next_v);
       } else {
 #pragma unroll
@@ -441,7 +458,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
       if (active(j)) {
         f32x16 s0, s1;
         scores(j, slot, s0, s1, next_k);
-        softmax(s0, s1, pbv);
+        softmax(j, s0, s1, pbv);
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q) next_k(q);
