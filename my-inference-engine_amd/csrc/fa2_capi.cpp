@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -37,32 +38,42 @@ int ok() {
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
-// Keys per split of the decode kernel: 4 waves x 32 keys at least, doubled until the grid holds at
-// most 4096 work-groups (16 per CU on 256 CUs, about half of them empty for rows shorter than the
-// longest), so long rows get enough parallelism while every wave still walks a few steps.  On
-// the 64-row U[128,8192] decode 256 keys measured best (128: -4%, 512: -15%).  MI_FA2_DECODE_CHUNK (a multiple of 128) overrides it,
-// for tuning sweeps.
-int decode_chunk(int64_t batch, int64_t heads_kv, int64_t max_kv) {
-  static const int forced = [] {
-    const char* env = std::getenv("MI_FA2_DECODE_CHUNK");
-    const int v = env ? std::atoi(env) : 0;
-    return (v >= 128 && v % 128 == 0) ? v : 0;
-  }();
-  if (forced) return forced;
-  int chunk = 128;
-  while (chunk < (1 << 16) && batch * heads_kv * ((max_kv + chunk - 1) / chunk) > 4096) chunk *= 2;
-  return chunk;
+// Decode work split: the kernel cuts every (row, kv head) item into 128-key chunks and gives each
+// of its work-groups an equal contiguous share of all the chunks (stream-K); an item cut by a share
+// boundary leaves one partial per work-group touching it.  Work-groups launched: 2 per CU of the
+// 256 on MI355X (each holds 4 waves of 256 VGPRs, so 2 fill a CU's register file), never more
+// than there are chunks.  MI_FA2_DECODE_WGS overrides it, for tuning sweeps.
+constexpr int kDecodeChunk = 128;
+
+// The split decode kernel serves one query per row, up to 16 query heads per kv head (the N of its
+// 16x16 MFMA) and up to 8192 rows (its row prefix sum lives in LDS); anything else runs through
+// the prefill kernel, which handles a single query row too.
+constexpr int kMaxDecodeBatch = 8192;
+bool uses_decode(int64_t seqlen_q, int64_t group, int64_t batch) {
+  return seqlen_q == 1 && group <= 16 && batch <= kMaxDecodeBatch;
 }
 
-int decode_splits(int64_t max_kv, int chunk) {
-  return max_kv > 0 ? (int)((max_kv + chunk - 1) / chunk) : 1;
+int decode_work_groups(int64_t batch, int64_t heads_kv, int64_t max_kv) {
+  static const int forced = [] {
+    const char* env = std::getenv("MI_FA2_DECODE_WGS");
+    const int v = env ? std::atoi(env) : 0;
+    return v > 0 ? v : 0;
+  }();
+  const int64_t chunks = batch * heads_kv * std::max<int64_t>(1, (max_kv + kDecodeChunk - 1) / kDecodeChunk);
+  const int64_t want = forced ? forced : 512;
+  return (int)std::max<int64_t>(1, std::min(want, chunks));
+}
+
+// Partial slots per (row, query head): at most one per chunk of the longest row.
+int decode_splits(int64_t max_kv) {
+  return max_kv > 0 ? (int)((max_kv + kDecodeChunk - 1) / kDecodeChunk) : 1;
 }
 
 // Workspace of a split decode: fp32 partial O [B][Hq][splits][128], m [B][Hq][splits] and
 // l [B][Hq][splits].
 size_t decode_workspace(int64_t batch, int64_t heads_q, int64_t heads_kv, int64_t max_kv) {
-  const int chunk = decode_chunk(batch, heads_kv, max_kv);
-  const int splits = decode_splits(max_kv, chunk);
+  (void)heads_kv;
+  const int splits = decode_splits(max_kv);
   if (splits <= 1) return 0;
   return (size_t)batch * heads_q * splits * (mi_fa2::kHeadDim + 2) * sizeof(float);
 }
@@ -132,7 +143,8 @@ const char* mi_fa2_last_error(void) { return g_err; }
 size_t mi_fa2_fwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv,
                                  int32_t seqlen_q, int32_t seqlen_k, int32_t head_dim) {
   (void)head_dim;
-  if (seqlen_q != 1 || heads_kv <= 0 || heads_q % heads_kv || heads_q / heads_kv > 16) return 0;
+  if (heads_kv <= 0 || heads_q % heads_kv || !uses_decode(seqlen_q, heads_q / heads_kv, batch))
+    return 0;
   return decode_workspace(batch, heads_q, heads_kv, seqlen_k);
 }
 
@@ -177,9 +189,9 @@ int mi_fa2_fwd(int32_t dtype, const void* q, const void* k, const void* v, void*
   p.scale_log2 = sm_scale * mi_fa2::kLog2e;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
-  if (seqlen_q == 1 && p.group <= 16) {
-    p.chunk = decode_chunk(batch, heads_kv, seqlen_k);
-    p.max_splits = decode_splits(seqlen_k, p.chunk);
+  if (uses_decode(seqlen_q, p.group, batch)) {
+    p.n_wg = decode_work_groups(batch, heads_kv, seqlen_k);
+    p.max_splits = decode_splits(seqlen_k);
     const size_t need = decode_workspace(batch, heads_q, heads_kv, seqlen_k);
     if (need) {
       if (!workspace || workspace_bytes < need)
@@ -285,9 +297,9 @@ int mi_fa2_fwd_paged(int32_t dtype, const void* q, const void* k_pool, const voi
   p.scale_log2 = sm_scale * mi_fa2::kLog2e;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
-  if (seqlen_q == 1 && p.group <= 16) {
-    p.chunk = decode_chunk(batch, heads_kv, max_kv_len);
-    p.max_splits = decode_splits(max_kv_len, p.chunk);
+  if (uses_decode(seqlen_q, p.group, batch)) {
+    p.n_wg = decode_work_groups(batch, heads_kv, max_kv_len);
+    p.max_splits = decode_splits(max_kv_len);
     const size_t need = decode_workspace(batch, heads_q, heads_kv, max_kv_len);
     if (need) {
       if (!workspace || workspace_bytes < need)

@@ -115,8 +115,8 @@ struct FwdParams {
   float* ws_o;
   float* ws_m;
   float* ws_l;
-  int32_t chunk;              // keys per split
-  int32_t max_splits;
+  int32_t n_wg;               // decode: work-groups launched
+  int32_t max_splits;         // decode: partial slots per (row, query head)
 };
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }

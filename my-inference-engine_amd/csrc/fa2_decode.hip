@@ -150,172 +150,249 @@ __device__ __forceinline__ void dc_compute(const DcStep& s, const u32x4 (&qb)[4]
   }
 }
 
-// Kernel shape knobs (compile-time; the defaults are the measured best on MI355X):
-//   MI_FA2_DC_HPW  kv heads per work-group (1 or 2): with 2, the two heads of a token -- one
-//                  contiguous 512-byte row of the cache -- are read by the same work-group at the
-//                  same time instead of by two work-groups at different times.
-//   MI_FA2_DC_PIPE 1 = two register buffers (next step's loads in flight during this step's math),
-//                  0 = one buffer and more resident waves instead.
-//   MI_FA2_DC_OCC  minimum waves per SIMD requested from the register allocator.
-//   MI_FA2_DC_NT   1 = K/V loads are non-temporal (streamed past the caches they would only evict).
-// Measured on the 64-row paged decode (kv_len U[128,8192], 256-key splits): HPW 1 vs 2 within
-// noise, PIPE 1 (256 VGPRs, 2 waves/SIMD) 15% slower than PIPE 0 (141 VGPRs, 3 waves/SIMD), NT
-// +2..4%.
-#ifndef MI_FA2_DC_HPW
-#define MI_FA2_DC_HPW 1
-#endif
-#ifndef MI_FA2_DC_PIPE
-#define MI_FA2_DC_PIPE 0
-#endif
-#ifndef MI_FA2_DC_OCC
-#define MI_FA2_DC_OCC 2
-#endif
+// Work split (stream-K over the keys of every (row, kv head) item).  Each item's keys are cut into
+// 128-key chunks (one 32-key step for each of the 4 waves); item i = (b, hk), hk fastest, owns
+// chunks [R[b] + hk*n_b, +n_b) of a global chunk sequence of length N, n_b = ceil(kv_len_b / 128)
+// (1 for an empty row, so that someone writes its zero output).  Work-group w of the W launched
+// takes the contiguous chunks [w*N/W', (w+1)*N/W'), W' = min(W, N): every work-group streams the
+// same number of bytes whatever the row lengths, there is no tail of short splits, and a work-group
+// that covers a whole item writes the final output.  Items cut by work-group boundaries get one fp32
+// partial per work-group touching them (at most n_b), merged by fa2_combine_kernel.  Work-groups
+// and the combine find the item boundaries from a prefix sum of the row chunk counts that every
+// work-group computes from kv_lens (B loads, one wave).
+constexpr int kDcChunk = kDcWaves * kDcStep;  // 128 keys
 
-template <typename E, int MODE, int HPW>
-__global__ __launch_bounds__(256, MI_FA2_DC_OCC) void fa2_decode_kernel(const FwdParams p) {
-  // Per-wave partials for the merge: O [wave][column][d], then m and l [wave][column].
+// First work-group (of W over N chunks) whose range contains chunk c.
+__device__ __forceinline__ int dc_first_wg(int64_t c, int64_t N, int W) {
+  return (int)(((c + 1) * W - 1) / N);
+}
+
+// Chunk counts of rows [0, B) prefix-summed into R[0..B] (LDS), by wave 0; R[B] is the number of
+// chunks per kv head summed over rows.  Ends with a barrier.
+__device__ __forceinline__ void dc_row_prefix(const FwdParams& p, int* R) {
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    int carry = 0;
+    if (lane == 0) R[0] = 0;
+    for (int base = 0; base < p.B; base += 64) {
+      const int b = base + lane;
+      int n = 0;
+      if (b < p.B) {
+        const int kv = p.kv_lens ? clamp_len(p.kv_lens[b], p.S) : p.S;
+        n = kv > 0 ? (kv + kDcChunk - 1) / kDcChunk : 1;
+      }
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(n, o);
+        if (lane >= o) n += t;
+      }
+      if (b < p.B) R[b + 1] = carry + n;
+      carry += __shfl(n, 63);
+    }
+  }
+  __syncthreads();
+}
+
+// The work-group's lds: the waves' partial (m, l, O) for the merge, then R[0..B].
+static size_t decode_lds_bytes(int group, int batch) {
+  return (size_t)kDcWaves * group * (kRedPitch + 2) * sizeof(float) + (size_t)(batch + 1) * 4;
+}
+
+template <typename E, int MODE>
+__global__ __launch_bounds__(256, 2) void fa2_decode_kernel(const FwdParams p, int n_wg) {
   extern __shared__ float red[];
   float* red_o = red;
   float* red_m = red + kDcWaves * p.group * kRedPitch;
   float* red_l = red_m + kDcWaves * p.group;
+  int* R = reinterpret_cast<int*>(red_l + kDcWaves * p.group);
 
-  const int split = blockIdx.x;
-  const int b = blockIdx.z;
-  const int kv_len = p.kv_lens ? clamp_len(p.kv_lens[b], p.S) : p.S;
-  const int n_splits = kv_len > 0 ? (kv_len + p.chunk - 1) / p.chunk : 1;
-  if (split >= n_splits) return;
-  const int k_begin = split * p.chunk;
-  const int k_end = min(kv_len, k_begin + p.chunk);
+  dc_row_prefix(p, R);
+  const int64_t N = (int64_t)R[p.B] * p.Hkv;
+  const int W = (int)min<int64_t>(n_wg, N);
+  const int w = blockIdx.x;
+  if (w >= W) return;
+  int64_t lo = (int64_t)w * N / W;
+  const int64_t hi = (int64_t)(w + 1) * N / W;
+
+  // Item containing chunk lo: binary search for the row, then the kv head.
+  int b = 0;
+  {
+    int l = 0, h = p.B;  // R[l] * Hkv <= lo < R[h] * Hkv
+    while (h - l > 1) {
+      const int m = (l + h) >> 1;
+      if ((int64_t)R[m] * p.Hkv <= lo) l = m; else h = m;
+    }
+    b = l;
+  }
+  int n_b = R[b + 1] - R[b];
+  int hk = (int)((lo - (int64_t)R[b] * p.Hkv) / n_b);
+  int c = (int)(lo - (int64_t)R[b] * p.Hkv - (int64_t)hk * n_b);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15;  // MFMA column: query head hk*group + n; also the A-operand row
   const int g = lane >> 4;  // lane group: k-slots 8g..8g+7
-  // Wave w serves kv head blockIdx.y*HPW + w%HPW and walks every (4/HPW)-th step of the split.
-  constexpr int kStreams = kDcWaves / HPW;
-  const int hk = blockIdx.y * HPW + wave % HPW;
-  const int stream = wave / HPW;
+  const float cl = p.scale_log2;
 
-  const int64_t k_off = (MODE == kDense ? (int64_t)b * p.k_sb : 0) + (int64_t)hk * p.k_sh;
-  const int64_t v_off = (MODE == kDense ? (int64_t)b * p.v_sb : 0) + (int64_t)hk * p.v_sh;
+  while (lo < hi) {
+    const int c_end = (int)min<int64_t>(n_b, c + (hi - lo));
+    const int kv_len = p.kv_lens ? clamp_len(p.kv_lens[b], p.S) : p.S;
+    const int k_begin = c * kDcChunk;
+    const int k_end = min(kv_len, c_end * kDcChunk);
 
-  // Q^T as the B operand of S^T = K Q^T: k-step ks covers d = 32*ks + 8*g + [0, 8).
-  u32x4 qb[4];
-  if (n < p.group) {
-    const uint16_t* qp = p.q + (int64_t)b * p.q_sb + (int64_t)(hk * p.group + n) * p.q_sh + g * 8;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qb[ks] = ld16(qp + ks * 32);
-  } else {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qb[ks] = u32x4{0, 0, 0, 0};
-  }
+    const int64_t k_off = (MODE == kDense ? (int64_t)b * p.k_sb : 0) + (int64_t)hk * p.k_sh;
+    const int64_t v_off = (MODE == kDense ? (int64_t)b * p.v_sb : 0) + (int64_t)hk * p.v_sh;
 
-  f32x4 oacc[8];
+    // Q^T as the B operand of S^T = K Q^T: k-step ks covers d = 32*ks + 8*g + [0, 8).
+    u32x4 qb[4];
+    if (n < p.group) {
+      const uint16_t* qp =
+          p.q + (int64_t)b * p.q_sb + (int64_t)(hk * p.group + n) * p.q_sh + g * 8;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) oacc[i] = f32x4{};
-  float m_run = -INFINITY;
-  float l_run = 0.f;
-  const float c = p.scale_log2;
-
-  constexpr int kStride = kStreams * kDcStep;
-  int kb = k_begin + stream * kDcStep;
-#if MI_FA2_DC_PIPE
-  // Software-pipelined walk (two register buffers): step s+1's loads fly during step s's math.
-  DcStep s0, s1;
-  if (kb < k_end) dc_load<MODE>(p, b, k_off, v_off, kb, k_end, n, g, s0);
-  while (kb < k_end) {
-    const int kb1 = kb + kStride;
-    if (kb1 < k_end) dc_load<MODE>(p, b, k_off, v_off, kb1, k_end, n, g, s1);
-    dc_compute<E>(s0, qb, kb, k_end, g, c, m_run, l_run, oacc);
-    if (kb1 >= k_end) break;
-    const int kb2 = kb1 + kStride;
-    if (kb2 < k_end) dc_load<MODE>(p, b, k_off, v_off, kb2, k_end, n, g, s0);
-    dc_compute<E>(s1, qb, kb1, k_end, g, c, m_run, l_run, oacc);
-    kb = kb2;
-  }
-#else
-  for (; kb < k_end; kb += kStride) {
-    DcStep s0;
-    dc_load<MODE>(p, b, k_off, v_off, kb, k_end, n, g, s0);
-    dc_compute<E>(s0, qb, kb, k_end, g, c, m_run, l_run, oacc);
-  }
-#endif
-
-  // Wave results to LDS. O^T accumulator r of d-block db is d = 8*(4g + r) + db, column n.
-  float l_w = l_run + __shfl_xor(l_run, 16);
-  l_w += __shfl_xor(l_w, 32);
-  if (n < p.group) {
-    float* ro = red_o + (wave * p.group + n) * kRedPitch;
-#pragma unroll
-    for (int db = 0; db < 8; ++db)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) ro[8 * (4 * g + r) + db] = oacc[db][r];
-    if (g == 0) {
-      red_m[wave * p.group + n] = m_run;
-      red_l[wave * p.group + n] = l_w;
-    }
-  }
-  __syncthreads();
-
-  // Merge the waves of each head: outputs (head sub-index, column, d).
-  const bool single = n_splits == 1;
-  for (int idx = tid; idx < HPW * p.group * kHeadDim; idx += 256) {
-    const int hs = idx / (p.group * kHeadDim);
-    const int col = (idx / kHeadDim) % p.group;
-    const int d = idx % kHeadDim;
-    float M = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kStreams; ++j) M = fmaxf(M, red_m[(hs + HPW * j) * p.group + col]);
-    const float M_use = M == -INFINITY ? 0.f : M;
-    float acc = 0.f, L = 0.f;
-#pragma unroll
-    for (int j = 0; j < kStreams; ++j) {
-      const int w = hs + HPW * j;
-      const float f = exp2_fast(red_m[w * p.group + col] - M_use);
-      acc += red_o[(w * p.group + col) * kRedPitch + d] * f;
-      L += red_l[w * p.group + col] * f;
-    }
-    const int hq = (blockIdx.y * HPW + hs) * p.group + col;
-    if (single) {
-      const float inv = L > 0.f ? 1.f / L : 0.f;
-      uint16_t* op = p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + d;
-      *op = (uint16_t)(E::pack2(acc * inv, 0.f) & 0xffffu);
-      if (p.lse && d == 0)
-        p.lse[(int64_t)b * p.l_sb + (int64_t)hq * p.l_sh] =
-            L > 0.f ? (M + __builtin_log2f(L)) * kLn2 : -INFINITY;
+      for (int ks = 0; ks < 4; ++ks) qb[ks] = ld16(qp + ks * 32);
     } else {
-      const int64_t slot = ((int64_t)b * p.Hq + hq) * p.max_splits + split;
-      p.ws_o[slot * kHeadDim + d] = acc;
-      if (d == 0) {
-        p.ws_m[slot] = M;
-        p.ws_l[slot] = L;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) qb[ks] = u32x4{0, 0, 0, 0};
+    }
+
+    f32x4 oacc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) oacc[i] = f32x4{};
+    float m_run = -INFINITY;
+    float l_run = 0.f;
+
+    // Software-pipelined walk (two register buffers): step s+1's loads fly during step s's math.
+    int kb = k_begin + wave * kDcStep;
+    DcStep s0, s1;
+    if (kb < k_end) dc_load<MODE>(p, b, k_off, v_off, kb, k_end, n, g, s0);
+    while (kb < k_end) {
+      const int kb1 = kb + kDcChunk;
+      if (kb1 < k_end) dc_load<MODE>(p, b, k_off, v_off, kb1, k_end, n, g, s1);
+      dc_compute<E>(s0, qb, kb, k_end, g, cl, m_run, l_run, oacc);
+      if (kb1 >= k_end) break;
+      const int kb2 = kb1 + kDcChunk;
+      if (kb2 < k_end) dc_load<MODE>(p, b, k_off, v_off, kb2, k_end, n, g, s0);
+      dc_compute<E>(s1, qb, kb1, k_end, g, cl, m_run, l_run, oacc);
+      kb = kb2;
+    }
+
+    // Wave results to LDS. O^T accumulator r of d-block db is d = 8*(4g + r) + db, column n.
+    float l_w = l_run + __shfl_xor(l_run, 16);
+    l_w += __shfl_xor(l_w, 32);
+    if (n < p.group) {
+      float* ro = red_o + (wave * p.group + n) * kRedPitch;
+#pragma unroll
+      for (int db = 0; db < 8; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ro[8 * (4 * g + r) + db] = oacc[db][r];
+      if (g == 0) {
+        red_m[wave * p.group + n] = m_run;
+        red_l[wave * p.group + n] = l_w;
       }
+    }
+    __syncthreads();
+
+    // Merge the 4 waves for each (column, d); finish the item here if this work-group covers all of
+    // it, otherwise leave a partial for the combine.
+    const bool whole = c == 0 && c_end == n_b;
+    const int64_t item_first = (int64_t)R[b] * p.Hkv + (int64_t)hk * n_b;
+    const int split = w - dc_first_wg(item_first, N, W);
+    for (int idx = tid; idx < p.group * kHeadDim; idx += 256) {
+      const int col = idx / kHeadDim;
+      const int d = idx % kHeadDim;
+      float M = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < kDcWaves; ++j) M = fmaxf(M, red_m[j * p.group + col]);
+      const float M_use = M == -INFINITY ? 0.f : M;
+      float acc = 0.f, L = 0.f;
+#pragma unroll
+      for (int j = 0; j < kDcWaves; ++j) {
+        const float f = exp2_fast(red_m[j * p.group + col] - M_use);
+        acc += red_o[(j * p.group + col) * kRedPitch + d] * f;
+        L += red_l[j * p.group + col] * f;
+      }
+      const int hq = hk * p.group + col;
+      if (whole) {
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        uint16_t* op = p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + d;
+        *op = (uint16_t)(E::pack2(acc * inv, 0.f) & 0xffffu);
+        if (p.lse && d == 0)
+          p.lse[(int64_t)b * p.l_sb + (int64_t)hq * p.l_sh] =
+              L > 0.f ? (M + __builtin_log2f(L)) * kLn2 : -INFINITY;
+      } else {
+        const int64_t slot = ((int64_t)b * p.Hq + hq) * p.max_splits + split;
+        p.ws_o[slot * kHeadDim + d] = acc;
+        if (d == 0) {
+          p.ws_m[slot] = M;
+          p.ws_l[slot] = L;
+        }
+      }
+    }
+    __syncthreads();  // red is rewritten by the next item
+
+    // Next item.
+    lo += c_end - c;
+    c = 0;
+    if (++hk == p.Hkv) {
+      hk = 0;
+      ++b;
+      if (b < p.B) n_b = R[b + 1] - R[b];
     }
   }
 }
 
-// Merges the split partials of rows that needed more than one split.  Grid (Hq, B), one thread
-// per head dimension; the splits are read 16 at a time with every load issued before any is
+// Merges the partials of items that were cut by work-group boundaries.  Grid (Hq, B), one thread
+// per head dimension; the partials are read 16 at a time with every load issued before any is
 // used, and folded in with an online log-sum-exp rescale.
 template <typename E>
-__global__ __launch_bounds__(kHeadDim) void fa2_combine_kernel(const FwdParams p) {
+__global__ __launch_bounds__(kHeadDim) void fa2_combine_kernel(const FwdParams p, int n_wg) {
   const int hq = blockIdx.x;
   const int b = blockIdx.y;
+  const int hk = hq / p.group;
+  // Chunk counts: rows before b (prefix) and row b, with the decode kernel's rule.
+  int before = 0;
+  for (int r = threadIdx.x; r < b; r += kHeadDim) {
+    const int kv = p.kv_lens ? clamp_len(p.kv_lens[r], p.S) : p.S;
+    before += kv > 0 ? (kv + kDcChunk - 1) / kDcChunk : 1;
+  }
+  int total = 0;
+  for (int r = threadIdx.x; r < p.B; r += kHeadDim) {
+    const int kv = p.kv_lens ? clamp_len(p.kv_lens[r], p.S) : p.S;
+    total += kv > 0 ? (kv + kDcChunk - 1) / kDcChunk : 1;
+  }
+  __shared__ int sums[2][kHeadDim / 64];
+  for (int o = 32; o >= 1; o >>= 1) {
+    before += __shfl_xor(before, o);
+    total += __shfl_xor(total, o);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    sums[0][threadIdx.x >> 6] = before;
+    sums[1][threadIdx.x >> 6] = total;
+  }
+  __syncthreads();
+  before = sums[0][0] + sums[0][1];
+  total = sums[1][0] + sums[1][1];
   const int kv_len = p.kv_lens ? clamp_len(p.kv_lens[b], p.S) : p.S;
-  const int n_splits = kv_len > 0 ? (kv_len + p.chunk - 1) / p.chunk : 1;
-  if (n_splits <= 1) return;
+  const int n_b = kv_len > 0 ? (kv_len + kDcChunk - 1) / kDcChunk : 1;
+  const int64_t N = (int64_t)total * p.Hkv;
+  const int W = (int)min<int64_t>(n_wg, N);
+  const int64_t first = (int64_t)before * p.Hkv + (int64_t)hk * n_b;
+  const int f = dc_first_wg(first, N, W);
+  const int l = dc_first_wg(first + n_b - 1, N, W);
+  const int n_parts = l - f + 1;
+  if (n_parts <= 1) return;  // the decode kernel wrote this row's output
   const int d = threadIdx.x;
   const int64_t base = ((int64_t)b * p.Hq + hq) * p.max_splits;
   float M = -INFINITY, L = 0.f, acc = 0.f;
-  for (int s0 = 0; s0 < n_splits; s0 += 16) {
-    float m[16], l[16], o[16];
+  for (int s0 = 0; s0 < n_parts; s0 += 16) {
+    float m[16], lv[16], o[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int s = s0 + i;
-      const bool ok = s < n_splits;
+      const bool ok = s < n_parts;
       m[i] = ok ? p.ws_m[base + s] : -INFINITY;
-      l[i] = ok ? p.ws_l[base + s] : 0.f;
+      lv[i] = ok ? p.ws_l[base + s] : 0.f;
       o[i] = ok ? p.ws_o[(base + s) * kHeadDim + d] : 0.f;
     }
     float Mn = M;
@@ -327,9 +404,9 @@ __global__ __launch_bounds__(kHeadDim) void fa2_combine_kernel(const FwdParams p
     acc *= sc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float f = exp2_fast(m[i] - Mu);
-      L += l[i] * f;
-      acc += o[i] * f;
+      const float f2 = exp2_fast(m[i] - Mu);
+      L += lv[i] * f2;
+      acc += o[i] * f2;
     }
     M = Mn;
   }
@@ -341,35 +418,24 @@ __global__ __launch_bounds__(kHeadDim) void fa2_combine_kernel(const FwdParams p
         L > 0.f ? (M + __builtin_log2f(L)) * kLn2 : -INFINITY;
 }
 
-// Dynamic LDS of the merge: O, m and l of every wave for the group's columns.
-static size_t decode_lds_bytes(int group) {
-  return (size_t)kDcWaves * group * (kRedPitch + 2) * sizeof(float);
-}
-
-template <typename E, int MODE, int HPW>
+template <typename E, int MODE>
 static hipError_t launch_decode_t(const FwdParams& p, hipStream_t stream) {
-  dim3 grid(p.max_splits, p.Hkv / HPW, p.B);
-  hipLaunchKernelGGL((fa2_decode_kernel<E, MODE, HPW>), grid, dim3(256),
-                     decode_lds_bytes(p.group), stream, p);
+  if (p.B == 0) return hipSuccess;
+  const int n_wg = p.n_wg;
+  hipLaunchKernelGGL((fa2_decode_kernel<E, MODE>), dim3(n_wg), dim3(256),
+                     decode_lds_bytes(p.group, p.B), stream, p, n_wg);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.max_splits <= 1) return err;
-  hipLaunchKernelGGL((fa2_combine_kernel<E>), dim3(p.Hq, p.B), dim3(kHeadDim), 0, stream, p);
+  hipLaunchKernelGGL((fa2_combine_kernel<E>), dim3(p.Hq, p.B), dim3(kHeadDim), 0, stream, p, n_wg);
   return hipGetLastError();
-}
-
-template <typename E, int MODE>
-static hipError_t launch_decode_m(const FwdParams& p, hipStream_t stream) {
-  if (p.B == 0) return hipSuccess;
-  if (MI_FA2_DC_HPW == 2 && p.Hkv % 2 == 0) return launch_decode_t<E, MODE, 2>(p, stream);
-  return launch_decode_t<E, MODE, 1>(p, stream);
 }
 
 hipError_t launch_decode(const FwdParams& p, int dtype, int mode, hipStream_t stream) {
   if (dtype == 0)
-    return mode == kPaged ? launch_decode_m<BF16, kPaged>(p, stream)
-                          : launch_decode_m<BF16, kDense>(p, stream);
-  return mode == kPaged ? launch_decode_m<FP16, kPaged>(p, stream)
-                        : launch_decode_m<FP16, kDense>(p, stream);
+    return mode == kPaged ? launch_decode_t<BF16, kPaged>(p, stream)
+                          : launch_decode_t<BF16, kDense>(p, stream);
+  return mode == kPaged ? launch_decode_t<FP16, kPaged>(p, stream)
+                        : launch_decode_t<FP16, kDense>(p, stream);
 }
 
 }  // namespace mi_fa2
