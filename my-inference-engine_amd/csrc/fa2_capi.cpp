@@ -40,9 +40,10 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 
 // Decode work split: the kernel cuts every (row, kv head) item into 128-key chunks and gives each
 // of its work-groups an equal contiguous share of all the chunks (stream-K); an item cut by a share
-// boundary leaves one partial per work-group touching it.  Work-groups launched: 2 per CU of the
-// 256 on MI355X (each holds 4 waves of 256 VGPRs, so 2 fill a CU's register file), never more
-// than there are chunks.  MI_FA2_DECODE_WGS overrides it, for tuning sweeps.
+// boundary leaves one partial per work-group touching it.  Work-groups launched: as many as fit on
+// the 256 CUs of MI355X at once (4 waves each: 2 per CU for the dense walk at 2 waves per SIMD, 3
+// per CU for the paged walk at 3 waves per SIMD), never more than there are chunks.
+// MI_FA2_DECODE_WGS overrides it, for tuning sweeps.
 constexpr int kDecodeChunk = 128;
 
 // The split decode kernel serves one query per row, up to 16 query heads per kv head (the N of its
@@ -53,14 +54,14 @@ bool uses_decode(int64_t seqlen_q, int64_t group, int64_t batch) {
   return seqlen_q == 1 && group <= 16 && batch <= kMaxDecodeBatch;
 }
 
-int decode_work_groups(int64_t batch, int64_t heads_kv, int64_t max_kv) {
+int decode_work_groups(int64_t batch, int64_t heads_kv, int64_t max_kv, bool paged) {
   static const int forced = [] {
     const char* env = std::getenv("MI_FA2_DECODE_WGS");
     const int v = env ? std::atoi(env) : 0;
     return v > 0 ? v : 0;
   }();
   const int64_t chunks = batch * heads_kv * std::max<int64_t>(1, (max_kv + kDecodeChunk - 1) / kDecodeChunk);
-  const int64_t want = forced ? forced : 512;
+  const int64_t want = forced ? forced : (paged ? 768 : 512);
   return (int)std::max<int64_t>(1, std::min(want, chunks));
 }
 
@@ -190,7 +191,7 @@ int mi_fa2_fwd(int32_t dtype, const void* q, const void* k, const void* v, void*
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
   if (uses_decode(seqlen_q, p.group, batch)) {
-    p.n_wg = decode_work_groups(batch, heads_kv, seqlen_k);
+    p.n_wg = decode_work_groups(batch, heads_kv, seqlen_k, false);
     p.max_splits = decode_splits(seqlen_k);
     const size_t need = decode_workspace(batch, heads_q, heads_kv, seqlen_k);
     if (need) {
@@ -298,7 +299,7 @@ int mi_fa2_fwd_paged(int32_t dtype, const void* q, const void* k_pool, const voi
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
   if (uses_decode(seqlen_q, p.group, batch)) {
-    p.n_wg = decode_work_groups(batch, heads_kv, max_kv_len);
+    p.n_wg = decode_work_groups(batch, heads_kv, max_kv_len, true);
     p.max_splits = decode_splits(max_kv_len);
     const size_t need = decode_workspace(batch, heads_q, heads_kv, max_kv_len);
     if (need) {
