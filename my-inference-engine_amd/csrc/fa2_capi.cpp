@@ -70,13 +70,13 @@ int decode_splits(int64_t max_kv) {
   return max_kv > 0 ? (int)((max_kv + kDecodeChunk - 1) / kDecodeChunk) : 1;
 }
 
-// Workspace of a split decode: fp32 partial O [B][Hq][splits][128], m [B][Hq][splits] and
-// l [B][Hq][splits].
+// Workspace of a split decode: fp32 partial O [B][Hq][splits][128], m [B][Hq][splits],
+// l [B][Hq][splits], then the int32 partial count of every (row, kv head) item [B][Hkv].
 size_t decode_workspace(int64_t batch, int64_t heads_q, int64_t heads_kv, int64_t max_kv) {
-  (void)heads_kv;
   const int splits = decode_splits(max_kv);
   if (splits <= 1) return 0;
-  return (size_t)batch * heads_q * splits * (mi_fa2::kHeadDim + 2) * sizeof(float);
+  return (size_t)batch * heads_q * splits * (mi_fa2::kHeadDim + 2) * sizeof(float) +
+         (size_t)batch * heads_kv * sizeof(int32_t);
 }
 
 void set_workspace(FwdParams& p, void* workspace) {
@@ -85,6 +85,7 @@ void set_workspace(FwdParams& p, void* workspace) {
   p.ws_o = ws;
   p.ws_m = ws + slots * mi_fa2::kHeadDim;
   p.ws_l = p.ws_m + slots;
+  p.ws_np = reinterpret_cast<int32_t*>(p.ws_l + slots);
 }
 
 int check_common(int32_t dtype, int32_t batch, int32_t heads_q, int32_t heads_kv,

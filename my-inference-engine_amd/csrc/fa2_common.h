@@ -115,6 +115,7 @@ struct FwdParams {
   float* ws_o;
   float* ws_m;
   float* ws_l;
+  int32_t* ws_np;             // decode: partials per (row, kv head) item, [B][Hkv]
   int32_t n_wg;               // decode: work-groups launched
   int32_t max_splits;         // decode: partial slots per (row, query head)
 };

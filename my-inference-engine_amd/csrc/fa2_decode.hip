@@ -316,7 +316,11 @@ __global__ __launch_bounds__(256, DcShape<MODE>::kOcc) void fa2_decode_kernel(co
     // it, otherwise leave a partial for the combine.
     const bool whole = c == 0 && c_end == n_b;
     const int64_t item_first = (int64_t)R[b] * p.Hkv + (int64_t)hk * n_b;
-    const int split = w - dc_first_wg(item_first, N, W);
+    const int f_wg = dc_first_wg(item_first, N, W);
+    const int split = w - f_wg;
+    // The item's first work-group records how many partials the combine has to merge (1: none).
+    if (split == 0 && tid == 0 && p.max_splits > 1)
+      p.ws_np[b * p.Hkv + hk] = dc_first_wg(item_first + n_b - 1, N, W) - f_wg + 1;
     for (int idx = tid; idx < p.group * kHeadDim; idx += 256) {
       const int col = idx / kHeadDim;
       const int d = idx % kHeadDim;
@@ -361,45 +365,15 @@ __global__ __launch_bounds__(256, DcShape<MODE>::kOcc) void fa2_decode_kernel(co
   }
 }
 
-// Merges the partials of items that were cut by work-group boundaries.  Grid (Hq, B), one thread
-// per head dimension; the partials are read 16 at a time with every load issued before any is
-// used, and folded in with an online log-sum-exp rescale.
+// Merges the partials of items that were cut by work-group boundaries (their count is recorded by
+// the decode kernel).  Grid (Hq, B), one thread per head dimension; the partials are read 16 at a
+// time with every load issued before any is used, and folded in with an online log-sum-exp
+// rescale.
 template <typename E>
-__global__ __launch_bounds__(kHeadDim) void fa2_combine_kernel(const FwdParams p, int n_wg) {
+__global__ __launch_bounds__(kHeadDim) void fa2_combine_kernel(const FwdParams p) {
   const int hq = blockIdx.x;
   const int b = blockIdx.y;
-  const int hk = hq / p.group;
-  // Chunk counts: rows before b (prefix) and row b, with the decode kernel's rule.
-  int before = 0;
-  for (int r = threadIdx.x; r < b; r += kHeadDim) {
-    const int kv = p.kv_lens ? clamp_len(p.kv_lens[r], p.S) : p.S;
-    before += kv > 0 ? (kv + kDcChunk - 1) / kDcChunk : 1;
-  }
-  int total = 0;
-  for (int r = threadIdx.x; r < p.B; r += kHeadDim) {
-    const int kv = p.kv_lens ? clamp_len(p.kv_lens[r], p.S) : p.S;
-    total += kv > 0 ? (kv + kDcChunk - 1) / kDcChunk : 1;
-  }
-  __shared__ int sums[2][kHeadDim / 64];
-  for (int o = 32; o >= 1; o >>= 1) {
-    before += __shfl_xor(before, o);
-    total += __shfl_xor(total, o);
-  }
-  if ((threadIdx.x & 63) == 0) {
-    sums[0][threadIdx.x >> 6] = before;
-    sums[1][threadIdx.x >> 6] = total;
-  }
-  __syncthreads();
-  before = sums[0][0] + sums[0][1];
-  total = sums[1][0] + sums[1][1];
-  const int kv_len = p.kv_lens ? clamp_len(p.kv_lens[b], p.S) : p.S;
-  const int n_b = kv_len > 0 ? (kv_len + kDcChunk - 1) / kDcChunk : 1;
-  const int64_t N = (int64_t)total * p.Hkv;
-  const int W = (int)min<int64_t>(n_wg, N);
-  const int64_t first = (int64_t)before * p.Hkv + (int64_t)hk * n_b;
-  const int f = dc_first_wg(first, N, W);
-  const int l = dc_first_wg(first + n_b - 1, N, W);
-  const int n_parts = l - f + 1;
+  const int n_parts = p.ws_np[b * p.Hkv + hq / p.group];
   if (n_parts <= 1) return;  // the decode kernel wrote this row's output
   const int d = threadIdx.x;
   const int64_t base = ((int64_t)b * p.Hq + hq) * p.max_splits;
@@ -445,7 +419,7 @@ static hipError_t launch_decode_t(const FwdParams& p, hipStream_t stream) {
                      decode_lds_bytes(p.group, p.B), stream, p, n_wg);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.max_splits <= 1) return err;
-  hipLaunchKernelGGL((fa2_combine_kernel<E>), dim3(p.Hq, p.B), dim3(kHeadDim), 0, stream, p, n_wg);
+  hipLaunchKernelGGL((fa2_combine_kernel<E>), dim3(p.Hq, p.B), dim3(kHeadDim), 0, stream, p);
   return hipGetLastError();
 }
 
