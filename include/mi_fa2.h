@@ -123,6 +123,30 @@ MI_FA2_API int mi_fa2_fwd_paged(int32_t dtype, const void* q, const void* k_pool
                      float sm_scale, void* workspace, size_t workspace_bytes,
                      mi_fa2_stream_t stream);
 
+/*
+ * Fused rotary embedding + paged KV-cache write, the step before attention.  Replaces apply_rope
+ * (model.py:62-65, applied at model.py:92) and KVCache.write (kv_cache.py:108-115, called at
+ * model.py:96) on the GPU path, with bitwise the same results (the reference's 16-bit rounding
+ * after each multiply and after the add):
+ *   qkv [n_tokens, (heads_q + 2*heads_kv) * 128] with row stride qkv_row_stride: the fused q|k|v
+ *     projection of every new token (q heads, then k heads, then v heads);
+ *   cos, sin [n_tokens, 128] with row stride cs_row_stride: the model's RoPE tables for each
+ *     token's position (model.py:151-155), in the same dtype;
+ *   slot_mapping [n_tokens] int32: the cache slot of each token (kv_cache.py:15-16); a slot outside
+ *     [0, num_slots) is skipped (a caller bug, guarded);
+ *   q_out [n_tokens, heads_q * 128] with row stride q_row_stride: receives the rotated q;
+ *   k_pool, v_pool: one layer of KVCache.buf (buf[layer, 0] and buf[layer, 1]), [num_slots,
+ *     heads_kv, 128] with pool_strides (slot, head): receive the rotated k and the v.
+ * Strides in elements, multiples of 8; pointers 16-byte aligned.  Asynchronous on `stream`.
+ */
+MI_FA2_API int mi_fa2_rope_kv_write(int32_t dtype, const void* qkv, int64_t qkv_row_stride,
+                                    const void* cos, const void* sin, int64_t cs_row_stride,
+                                    const int32_t* slot_mapping, int32_t n_tokens, int32_t heads_q,
+                                    int32_t heads_kv, int32_t head_dim, void* q_out,
+                                    int64_t q_row_stride, void* k_pool, void* v_pool,
+                                    const int64_t* pool_strides, int32_t num_slots,
+                                    mi_fa2_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

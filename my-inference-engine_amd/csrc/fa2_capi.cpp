@@ -15,6 +15,7 @@ namespace mi_fa2 {
 hipError_t launch_prefill(const FwdParams& p, int dtype, int mode, int max_seqlen_q,
                           hipStream_t stream);
 hipError_t launch_decode(const FwdParams& p, int dtype, int mode, hipStream_t stream);
+hipError_t launch_rope_kv(const RopeParams& p, int dtype, hipStream_t stream);
 }  // namespace mi_fa2
 
 using mi_fa2::FwdParams;
@@ -315,3 +316,54 @@ int mi_fa2_fwd_paged(int32_t dtype, const void* q, const void* k_pool, const voi
 }
 
 }  // extern "C"
+
+
+int mi_fa2_rope_kv_write(int32_t dtype, const void* qkv, int64_t qkv_row_stride, const void* cos,
+                         const void* sin, int64_t cs_row_stride, const int32_t* slot_mapping,
+                         int32_t n_tokens, int32_t heads_q, int32_t heads_kv, int32_t head_dim,
+                         void* q_out, int64_t q_row_stride, void* k_pool, void* v_pool,
+                         const int64_t* pool_strides, int32_t num_slots, mi_fa2_stream_t stream) {
+  if (dtype != MI_FA2_BF16 && dtype != MI_FA2_FP16)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "dtype %d is not bf16 (0) or fp16 (1)", dtype);
+  if (head_dim != mi_fa2::kHeadDim)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "head_dim %d: the kernel is built for head_dim 128", head_dim);
+  if (n_tokens < 0 || heads_q <= 0 || heads_kv <= 0 || num_slots < 0)
+    return fail(MI_FA2_ERR_INVALID, "bad sizes: n_tokens=%d heads_q=%d heads_kv=%d num_slots=%d",
+                n_tokens, heads_q, heads_kv, num_slots);
+  if (n_tokens == 0) return ok();
+  const void* ptrs[] = {qkv, cos, sin, q_out, k_pool, v_pool};
+  const char* names[] = {"qkv", "cos", "sin", "q_out", "k_pool", "v_pool"};
+  for (int i = 0; i < 6; ++i) {
+    if (!ptrs[i]) return fail(MI_FA2_ERR_INVALID, "%s is NULL", names[i]);
+    if (!aligned16(ptrs[i])) return fail(MI_FA2_ERR_INVALID, "%s is not 16-byte aligned", names[i]);
+  }
+  if (!slot_mapping) return fail(MI_FA2_ERR_INVALID, "slot_mapping is NULL");
+  if (!pool_strides) return fail(MI_FA2_ERR_INVALID, "pool strides are NULL");
+  const int64_t strides[] = {qkv_row_stride, cs_row_stride, q_row_stride, pool_strides[0],
+                             pool_strides[1]};
+  for (int64_t st : strides)
+    if (st <= 0 || st % 8)
+      return fail(MI_FA2_ERR_INVALID, "stride %lld is not a positive multiple of 8 elements",
+                  (long long)st);
+  if (qkv_row_stride < (int64_t)(heads_q + 2 * heads_kv) * mi_fa2::kHeadDim ||
+      cs_row_stride < mi_fa2::kHeadDim || q_row_stride < (int64_t)heads_q * mi_fa2::kHeadDim)
+    return fail(MI_FA2_ERR_INVALID, "row strides shorter than a row");
+  mi_fa2::RopeParams p{};
+  p.qkv = static_cast<const uint16_t*>(qkv);
+  p.qkv_st = qkv_row_stride;
+  p.cos = static_cast<const uint16_t*>(cos);
+  p.sin = static_cast<const uint16_t*>(sin);
+  p.cs_st = cs_row_stride;
+  p.slots = slot_mapping;
+  p.q_out = static_cast<uint16_t*>(q_out);
+  p.q_st = q_row_stride;
+  p.k_pool = static_cast<uint16_t*>(k_pool);
+  p.v_pool = static_cast<uint16_t*>(v_pool);
+  p.pool_st = pool_strides[0];
+  p.pool_sh = pool_strides[1];
+  p.num_slots = num_slots;
+  p.n_tokens = n_tokens;
+  p.Hq = heads_q;
+  p.Hkv = heads_kv;
+  return launched(mi_fa2::launch_rope_kv(p, dtype, reinterpret_cast<hipStream_t>(stream)));
+}

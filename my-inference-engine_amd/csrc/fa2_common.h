@@ -120,6 +120,23 @@ struct FwdParams {
   int32_t max_splits;         // decode: partial slots per (row, query head)
 };
 
+// Everything the fused RoPE + KV-write launch needs (rope_kv.hip).
+struct RopeParams {
+  const uint16_t* qkv;  // [n_tokens][qkv_st]: q heads, then k heads, then v heads, 128 each
+  int64_t qkv_st;
+  const uint16_t* cos;  // [n_tokens][cs_st] (128 used)
+  const uint16_t* sin;
+  int64_t cs_st;
+  const int32_t* slots;  // [n_tokens] cache slot of each token
+  uint16_t* q_out;       // [n_tokens][q_st]: rotated q heads, 128 each
+  int64_t q_st;
+  uint16_t* k_pool;  // [num_slots][pool_sh * heads_kv]: token-major cache layer
+  uint16_t* v_pool;
+  int64_t pool_st, pool_sh;
+  int32_t num_slots;
+  int32_t n_tokens, Hq, Hkv;
+};
+
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 // Raw buffer resource over [base, base + bytes): loads at offsets past `bytes` return zeros, which

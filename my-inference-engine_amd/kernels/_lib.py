@@ -33,6 +33,8 @@ SIGNATURES = {
     "mi_fa2_fwd_varlen": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32,
                                  _p, _p, _p, _p, _p, _i32, _f32, _p]),
     "mi_fa2_fwd_paged_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "mi_fa2_rope_kv_write": (_i32, [_i32, _p, _i64, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _p,
+                                    _i64, _p, _p, _p, _i32, _p]),
     "mi_fa2_fwd_paged": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32,
                                 _i32, _i32, _i32, _i32, _p, _p, _p, _p, _i32, _f32, _p, _sz, _p]),
 }

@@ -36,6 +36,7 @@ class StepMeta:
     kv_lens: torch.Tensor        # [B] int32 = starts + T
     slot_mapping: torch.Tensor   # [B*T] int64, row-major (row, t)
     block_table: torch.Tensor    # [B, W] int32
+    slot_mapping32: torch.Tensor = None  # the same slots as int32 (for the fused RoPE + write)
     tables: list = field(default_factory=list)  # host copies of the rows' block lists
 
     @property
@@ -142,6 +143,7 @@ class KVCache:
             starts_dev=dev[:B], kv_lens=dev[B:2 * B],
             block_table=dev[2 * B:2 * B + B * W].view(B, W),
             slot_mapping=dev[2 * B + B * W:].long(),
+            slot_mapping32=dev[2 * B + B * W:],
             tables=[list(t) for t in tables])
 
     # -- data movement --------------------------------------------------------------------------

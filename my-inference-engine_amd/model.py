@@ -9,6 +9,8 @@ logits (model.py:204-207) -- with two deliberate differences on the GPU path:
     instead of gathering a dense copy every layer of every step (KVCache.read, kv_cache.py:117-121,
     called at model.py:97) and then calling the padded kernel (model.py:103).
   * The q/k/v and gate/up projections are single fused GEMMs (one launch instead of three/two).
+  * RoPE and the cache write are one HIP launch (kernels.rope.rope_kv_write) instead of the
+    elementwise RoPE ops and two index_copy_ (model.py:92,96), with bitwise the same results.
 
 On CPU tensors the model takes the reference's own fallback (dense read + fp32 SDPA with the
 bottom-right mask, model.py:104-107,181-195), which only the CPU tests of the scheduler use; the
@@ -21,6 +23,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from kernels.fa2 import fa2_paged
+from kernels.rope import rope_kv_write
 
 
 @dataclass(frozen=True)
@@ -82,17 +85,24 @@ class Attention(nn.Module):
     def forward(self, x, cos, sin, cache, layer, meta):
         cfg = self.cfg
         B, T, _ = x.shape
-        q, k, v = self.qkv_proj(x).split([self.q_size, self.kv_size, self.kv_size], dim=-1)
-        q = q.view(B, T, cfg.num_heads, cfg.head_dim).transpose(1, 2)
-        k = k.view(B, T, cfg.num_kv_heads, cfg.head_dim).transpose(1, 2)
-        v = v.view(B, T, cfg.num_kv_heads, cfg.head_dim).transpose(1, 2)
-        q, k = apply_rope(q, k, cos, sin)
-        cache.write(layer, meta, k, v)
+        qkv = self.qkv_proj(x)
         if x.is_cuda:
+            # rotated q out, rotated k and v into their cache slots, in one launch
+            q = rope_kv_write(qkv.view(B * T, -1), cos[:, 0].reshape(B * T, cfg.head_dim),
+                              sin[:, 0].reshape(B * T, cfg.head_dim), meta.slot_mapping32,
+                              cache.k_pool(layer), cache.v_pool(layer), cfg.num_heads,
+                              cfg.num_kv_heads)
+            q = q.view(B, T, cfg.num_heads, cfg.head_dim).transpose(1, 2)
             out = fa2_paged(q, cache.k_pool(layer), cache.v_pool(layer), meta.block_table,
                             meta.kv_lens, block_size=cache.block_size, max_kv_len=meta.max_kv,
                             is_causal=T > 1)
         else:
+            q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
+            q = q.view(B, T, cfg.num_heads, cfg.head_dim).transpose(1, 2)
+            k = k.view(B, T, cfg.num_kv_heads, cfg.head_dim).transpose(1, 2)
+            v = v.view(B, T, cfg.num_kv_heads, cfg.head_dim).transpose(1, 2)
+            q, k = apply_rope(q, k, cos, sin)
+            cache.write(layer, meta, k, v)
             k_all, v_all = cache.read(layer, meta)
             n_rep = cfg.num_heads // cfg.num_kv_heads
             out = F.scaled_dot_product_attention(q, repeat_kv(k_all, n_rep), repeat_kv(v_all, n_rep),

@@ -16,6 +16,9 @@ reference):
   paged.build_pool       a KVCache-layout pool + per-row block tables from dense K/V.
   brute.attention_f64    float64 loops over (row, head, query, key): the textbook definition,
                          used to pin sdpa.attention_ref on small shapes.
+  rope.apply_rope        rotate-half RoPE in the tensor dtype (model.py:58-65) and its cos/sin
+  rope.rope_cos_sin      tables (model.py:151-155); rope.cache_write, the cache scatter
+  rope.cache_write       (kv_cache.py:108-115).
 
 The seeded workload generators are not part of the oracle: they live in the package
 (my-inference-engine_amd/workloads.py) because bench.py's GPU leg needs them too.
