@@ -101,13 +101,16 @@ def bench_decode(steps, warmup, rotate_bytes=2 << 30):
     return ms, wl.decode_bytes(lens), lens, copies
 
 
-def bench_e2e(n_chats=16, reply_tokens=64, lo=32, hi=1000, seed=0):
+def bench_e2e(n_chats=16, reply_tokens=64, lo=32, hi=1000, seed=0, decode_graphs=True):
     """End-to-end serving of the Qwen2.5-1.5B architecture (28 layers, hidden 1536, 12q/2kv, head_dim
     128, SwiGLU 8960, vocab 151936, RoPE theta 1e6, tied embeddings) with random N(0, 0.02) bf16
     weights: n_chats conversations submitted at once, prompts of U[lo, hi] random token ids, each
     replying exactly reply_tokens tokens (no EOS) with seeded temperature-1 sampling, paged KV in
     16-token blocks under a 448 MiB budget (1024 blocks).  tok/s = generated tokens / wall time from
-    the first submit to the last finish (metrics/benchmark_concurrency.py:57-76,166-172)."""
+    the first submit to the last finish (metrics/benchmark_concurrency.py:57-76,166-172).
+
+    With decode_graphs the decode steps replay HIP graphs captured once before the run (batch
+    buckets 1..n_chats); the capture time is reported, not counted, like a server's start-up."""
     import torch
     from engine import Engine, run_concurrent_chats
     from kv_cache import KVCache
@@ -119,13 +122,23 @@ def bench_e2e(n_chats=16, reply_tokens=64, lo=32, hi=1000, seed=0):
     model = model.to(torch.bfloat16).eval()
     cache = KVCache(1024, 16, "cuda", torch.bfloat16, cfg.num_layers, cfg.num_kv_heads, cfg.head_dim)
     kv_mib = cache.buf.numel() * cache.buf.element_size() / 2**20
-    eng = Engine(model, cache, max_reply_tokens=reply_tokens, temperature=1.0, seed=seed)
+    graphs, capture_s = None, 0.0
+    if decode_graphs:
+        from graphs import DecodeGraphs
+        t0 = time.perf_counter()
+        buckets = tuple(b for b in (1, 2, 4, 8, 16, 32, 64) if b < n_chats) + (n_chats,)
+        graphs = DecodeGraphs(model, cache, buckets=buckets)
+        torch.cuda.synchronize()
+        capture_s = time.perf_counter() - t0
+    eng = Engine(model, cache, max_reply_tokens=reply_tokens, temperature=1.0, seed=seed,
+                 decode_graphs=graphs)
     g = torch.Generator().manual_seed(seed)
     lens = torch.randint(lo, hi + 1, (n_chats,), generator=g).tolist()
     prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in lens]
     run_concurrent_chats(eng, prompts[:1], reply_tokens=2)   # warm-up (one chat, two tokens)
     summary = run_concurrent_chats(eng, prompts, reply_tokens)
-    summary.update(prompt_lens_sum=sum(lens), kv_mib=kv_mib)
+    summary.update(prompt_lens_sum=sum(lens), kv_mib=kv_mib, decode_graphs=bool(graphs),
+                   graph_capture_s=capture_s)
     return summary
 
 

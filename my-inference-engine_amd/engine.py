@@ -49,9 +49,10 @@ class Job:
 
 class Engine:
     def __init__(self, model, cache, *, max_reply_tokens=512, temperature=1.0, sep_ids=(198,),
-                 seed=0):
+                 seed=0, decode_graphs=None):
         self.model = model
         self.cache = cache
+        self.decode_graphs = decode_graphs  # graphs.DecodeGraphs, or None: eager decode steps
         self.max_reply_tokens = max_reply_tokens
         self.temperature = temperature
         self.sep_ids = list(sep_ids)   # appended after each reply, like "\n" (chat.py:200)
@@ -186,10 +187,14 @@ class Engine:
         if not continuing:
             return
         seqs = [j.conv.seq for j in continuing]
-        input_ids = torch.tensor([[j.next_token] for j in continuing], device=self.device)
-        with torch.no_grad():
-            logits = self.model(input_ids, self.cache, seqs)
-        for job, tok in zip(continuing, self._sample(logits[:, -1])):
+        graphs = self.decode_graphs
+        if graphs is not None and len(seqs) <= graphs.max_rows:
+            last = graphs.run(seqs, [j.next_token for j in continuing])
+        else:
+            input_ids = torch.tensor([[j.next_token] for j in continuing], device=self.device)
+            with torch.no_grad():
+                last = self.model(input_ids, self.cache, seqs)[:, -1]
+        for job, tok in zip(continuing, self._sample(last)):
             job.next_token = tok
 
     def _sample(self, logits):

@@ -57,16 +57,17 @@ _WORKSPACES = {}
 
 
 def _workspace(nbytes, device):
-    """The split-decode workspace of (device, current stream): zero-filled once, grown on demand.
+    """The split-decode workspace of (device, current stream), grown on demand.
 
-    The kernels leave its counter region at zero when they finish, so it is reused across calls
-    without clearing; one buffer per stream keeps calls on different streams from sharing it."""
+    Its contents need no initialisation (every partial the combine reads is written by the same
+    launch), so it is allocated uninitialised -- no fill, which also keeps a captured graph free of
+    memset nodes; one buffer per stream keeps calls on different streams from sharing it."""
     if not nbytes:
         return None
     key = (device, torch.cuda.current_stream(device).cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(int(nbytes), dtype=torch.uint8, device=device)
+        ws = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
 

@@ -38,10 +38,11 @@ class StepMeta:
     block_table: torch.Tensor    # [B, W] int32
     slot_mapping32: torch.Tensor = None  # the same slots as int32 (for the fused RoPE + write)
     tables: list = field(default_factory=list)  # host copies of the rows' block lists
+    kv_cap: int = None           # fixed upper bound of kv_lens (captured decode graphs)
 
     @property
     def max_kv(self):
-        return max(self.starts) + self.T
+        return self.kv_cap if self.kv_cap is not None else max(self.starts) + self.T
 
     def gather_idx(self, device):
         """[B, S] physical slot of every logical position [0, max_kv) (kv_cache.py:93-98)."""
@@ -113,33 +114,48 @@ class KVCache:
             self._lengths[s] += T
 
     # -- per-step metadata ----------------------------------------------------------------------
-    def prepare(self, seqs, T):
+    def pack_step(self, seqs, T, W=None, out=None, rows=None):
+        """Grow the rows' tables for T new tokens and pack the step's metadata into one int32 host
+        array [starts | kv_lens | block_table rows*W | slot_mapping rows*T] (kv_cache.py:74-101).
+
+        W defaults to the blocks the longest row needs; `rows` >= len(seqs) pads the batch with
+        empty rows (no keys, slot -1: nothing read or written).  Returns (array, starts, W)."""
         bs = self.block_size
         starts = [self._lengths[s] for s in seqs]
         for s, start in zip(seqs, starts):
             self.ensure_capacity(s, start + T)
         B = len(seqs)
-        W = max(1, math.ceil((max(starts) + T) / bs))
+        R = rows or B
+        W = W or max(1, math.ceil((max(starts) + T) / bs))
         tables = [self._block_tables[s] for s in seqs]
-        # one int32 host array: [starts | kv_lens | block_table B*W | slot_mapping B*T]
-        host = np.zeros(2 * B + B * W + B * T, dtype=np.int32)
+        n_all = 2 * R + R * W + R * T
+        host = np.zeros(n_all, dtype=np.int32) if out is None else out[:n_all]
+        if out is not None:
+            host.fill(0)
         st = np.asarray(starts, dtype=np.int32)
         host[:B] = st
-        host[B:2 * B] = st + T
-        bt = host[2 * B:2 * B + B * W].reshape(B, W)
+        host[R:R + B] = st + T
+        bt = host[2 * R:2 * R + R * W].reshape(R, W)
         for i, t in enumerate(tables):
             n = min(len(t), W)
             bt[i, :n] = t[:n]
         pos = st[:, None] + np.arange(T, dtype=np.int32)[None, :]        # [B, T]
-        rows = np.arange(B)[:, None]
-        host[2 * B + B * W:] = (bt[rows, pos // bs] * bs + pos % bs).reshape(-1)
+        sm = host[2 * R + R * W:].reshape(R, T)
+        sm[:B] = bt[np.arange(B)[:, None], pos // bs] * bs + pos % bs
+        sm[B:] = -1
+        return host, starts, W
+
+    def prepare(self, seqs, T):
+        B = len(seqs)
+        host, starts, W = self.pack_step(seqs, T)
+        tables = [self._block_tables[s] for s in seqs]
         cpu = torch.from_numpy(host)
         if self.device.type == "cuda":
             dev = cpu.pin_memory().to(self.device, non_blocking=True)
         else:
             dev = cpu.clone()
         return StepMeta(
-            starts=starts, T=T, block_size=bs,
+            starts=starts, T=T, block_size=self.block_size,
             starts_dev=dev[:B], kv_lens=dev[B:2 * B],
             block_table=dev[2 * B:2 * B + B * W].view(B, W),
             slot_mapping=dev[2 * B + B * W:].long(),

@@ -167,12 +167,19 @@ class Qwen2ForCausalLM(nn.Module):
         """input_ids [B, T] appended to cache sequences `seqs`; returns last-position logits
         [B, 1, vocab] (model.py:157-207)."""
         _, T = input_ids.shape
-        x = self.embed_tokens(input_ids)
         meta = cache.prepare(seqs, T)
+        logits = self.forward_meta(input_ids, cache, meta)
+        cache.advance(seqs, T)
+        return logits
+
+    def forward_meta(self, input_ids, cache, meta):
+        """The layers over an already prepared step: what a captured decode graph replays, its
+        metadata living in static device buffers."""
+        _, T = input_ids.shape
+        x = self.embed_tokens(input_ids)
         position_ids = meta.starts_dev[:, None] + torch.arange(T, device=x.device)[None, :]
         cos, sin = self.rope_cos_sin(position_ids, x.dtype)
         for layer_idx, layer in enumerate(self.layers):
             x = layer(x, cos, sin, cache, layer_idx, meta)
-        cache.advance(seqs, T)
         x = self.norm(x[:, -1:])
         return x @ self.embed_tokens.weight.T

@@ -56,3 +56,51 @@ def test_gpu_concurrent_chats_complete():
     summary = run_concurrent_chats(eng, prompts, reply_tokens=8)
     assert summary["tokens"] == 32
     assert cache.free_block_count() == 128
+
+
+def test_captured_decode_graphs_match_eager_decode():
+    """Graph replays (padded buckets, static metadata) give the eager decode's logits and cache."""
+    from graphs import DecodeGraphs
+    g = torch.Generator().manual_seed(3)
+    prompts = [torch.randint(0, SMALL.vocab_size, (1, n), generator=g) for n in (37, 150, 5, 64, 20)]
+    toks = torch.randint(0, SMALL.vocab_size, (5, 4), generator=g)
+    em, ec = make("cuda", torch.bfloat16)
+    gm, gc = make("cuda", torch.bfloat16)
+    announce("[gpu] decode graphs: capture")
+    graphs = DecodeGraphs(gm, gc, buckets=(1, 2, 4, 8))
+    es = [ec.alloc() for _ in prompts]
+    gs = [gc.alloc() for _ in prompts]
+    with torch.no_grad():
+        for p, a, b in zip(prompts, es, gs):
+            em(p.cuda(), ec, [a])
+            gm(p.cuda(), gc, [b])
+        # batches of 3, 2 (bucket 2), 5 (bucket 8) and 1 rows
+        for t, rows in enumerate(([0, 1, 2], [3, 4], [0, 1, 2, 3, 4], [2])):
+            announce(f"[gpu] decode graphs: step {t} rows {rows}")
+            want = em(toks[rows, t:t + 1].cuda(), ec, [es[i] for i in rows])[:, -1].float()
+            got = graphs.run([gs[i] for i in rows], toks[rows, t].tolist()).float()
+            torch.cuda.synchronize()
+            scale = want.abs().max().item()
+            assert (got - want).abs().max().item() <= 0.02 * scale, t
+    assert [ec.length(s) for s in es] == [gc.length(s) for s in gs]
+    # the new tokens' K/V went to the same places in both caches (close, not bitwise: the
+    # attention outputs of the first layer feed the second layer's projections)
+    for i in range(len(prompts)):
+        ta, tb = ec._block_tables[es[i]], gc._block_tables[gs[i]]
+        n = ec.length(es[i])
+        ka = ec.buf[:, :, torch.tensor([ta[p // 16] * 16 + p % 16 for p in range(n)])].float()
+        kb = gc.buf[:, :, torch.tensor([tb[p // 16] * 16 + p % 16 for p in range(n)])].float()
+        assert (ka - kb).abs().max().item() <= 0.02 * ka.abs().max().item()
+
+
+def test_engine_with_decode_graphs_completes():
+    from graphs import DecodeGraphs
+    model, cache = make("cuda", torch.bfloat16, num_blocks=128)
+    graphs = DecodeGraphs(model, cache, buckets=(1, 2, 4))
+    eng = Engine(model, cache, max_reply_tokens=8, seed=0, decode_graphs=graphs)
+    g = torch.Generator().manual_seed(4)
+    prompts = [torch.randint(0, SMALL.vocab_size, (n,), generator=g).tolist() for n in (40, 7, 300, 96)]
+    announce("[gpu] 4 concurrent chats x 8 tokens, decode graphs")
+    summary = run_concurrent_chats(eng, prompts, reply_tokens=8)
+    assert summary["tokens"] == 32
+    assert cache.free_block_count() == 128
