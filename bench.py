@@ -1,6 +1,7 @@
 """Benchmark of the MI355X attention hot path; prints one JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary] [--no-e2e]
+                    [--only prefill|decode|ragged|copy]
 
 A "step" is one call of the hot path on one batch of synthetic input, inputs resident in HBM:
 
@@ -17,6 +18,10 @@ Timing: W untimed warmup steps, then torch.cuda.synchronize(); a HIP event pair 
 kernels are launched on brackets exactly K steps; synchronize.  The per-launch duration is the
 event time / K.  The CPU baseline is the fp32 SDPA oracle (the reference's fallback path) on the
 same inputs, on this host's cores, median of 5 runs.
+
+--only runs one workload alone (for counter profiles: one kernel family per process); `copy` is a
+1 GiB device-to-device copy of known size, the calibration for the FETCH_SIZE / WRITE_SIZE
+counters.
 
 One GPU only: --gpus N > 1 exits with a message.
 """
@@ -184,6 +189,33 @@ def cpu_decode_baseline(runs=3):
     return wl.decode_bytes(lens) / sec / 1e9, torch.get_num_threads(), sec
 
 
+def bench_copy(steps, warmup, nbytes=1 << 30):
+    """A plain 1 GiB device copy: reads and writes exactly nbytes per launch."""
+    import torch
+    src = torch.ones(nbytes // 2, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    ms = _time_gpu(lambda i=0: dst.copy_(src), steps, warmup)
+    return ms, nbytes
+
+
+def run_only(which, steps, warmup):
+    """One workload alone, one JSON line with its time per launch."""
+    if which == "prefill":
+        ms, flops = bench_prefill(steps, warmup)
+        rate, unit = flops / (ms * 1e-3) / 1e12, "TFLOP/s"
+    elif which == "decode":
+        ms, nbytes, _, _ = bench_decode(steps, warmup)
+        rate, unit = nbytes / (ms * 1e-3) / 1e9, "GB/s"
+    elif which == "ragged":
+        ms, flops, _ = bench_ragged(steps, warmup)
+        rate, unit = flops / (ms * 1e-3) / 1e12, "TFLOP/s"
+    else:
+        ms, nbytes = bench_copy(steps, warmup)
+        rate, unit = 2 * nbytes / (ms * 1e-3) / 1e9, "GB/s"
+    print(json.dumps({"only": which, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 5),
+                      "value": round(rate, 2), "unit": unit}), flush=True)
+
+
 def read_traffic(name):
     """HBM bytes per launch recorded by the rocprofv3 --pmc summaries under profiles/, if any."""
     path = ROOT / "profiles" / "traffic.json"
@@ -203,6 +235,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-secondary", action="store_true", help="prefill headline only")
     ap.add_argument("--no-e2e", action="store_true", help="skip the 16-chat end-to-end run")
+    ap.add_argument("--only", choices=("prefill", "decode", "ragged", "copy"),
+                    help="run one workload alone (counter profiles)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's hot path runs on a single MI355X "
@@ -211,6 +245,9 @@ def main():
 
     import torch
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.only:
+        run_only(args.only, args.steps, args.warmup)
+        return
 
     ms, flops = bench_prefill(args.steps, args.warmup)
     tflops = flops / (ms * 1e-3) / 1e12
