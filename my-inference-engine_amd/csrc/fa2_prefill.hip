@@ -146,6 +146,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   int kv_hi = kv_len;
   if (p.causal) kv_hi = min(kv_len, min(q0 + kPfRows, T_b) + off);
   if (kv_hi < 0) kv_hi = 0;
+  kv_hi = __builtin_amdgcn_readfirstlane(kv_hi);  // uniform: keeps the load arithmetic scalar
   const int n_steps = (kv_hi + kPfStep - 1) / kPfStep;
 
   // This wave's rows and the key ranges they need.
@@ -226,8 +227,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
       lds_dma16(uniform_u64(reinterpret_cast<uint64_t>(ptr)),
                 __builtin_amdgcn_readfirstlane(n * (int)st * 2), lds, voff);
     } else {
+      // Scalar selects only (no branch in the middle of the MFMA phases that issue these).
       const int t0 = max(ts, 0);
-      const int rows = ts < 0 ? 0 : sclamp(kv_hi - ts, 0, kPfBc);
+      int rows = min(kv_hi - ts, kPfBc);
+      rows = ts < 0 ? 0 : rows;
+      rows = max(rows, 0);
       lds_dma16(uniform_u64(reinterpret_cast<uint64_t>(base + off + (int64_t)t0 * st)),
                 __builtin_amdgcn_readfirstlane(rows * (int)st * 2), lds,
                 voff + h * 32 * (int)st * 2);
@@ -295,6 +299,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
       s0 = E::mfma32(ka[s % 3][0], qb[s], s0);
       s1 = E::mfma32(ka[s % 3][1], qb[s], s1);
       if (s & 1) dma(s >> 1);
+      // Keep the reads two k-steps ahead: left alone, the scheduler sinks each read to just
+      // before its MFMA, which then waits the whole LDS latency.
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
@@ -395,6 +402,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
 #pragma unroll
       for (int db = 0; db < 4; ++db) oacc[db] = E::mfma32(va[kk & 1][db], pb[kk], oacc[db]);
       dma(kk);
+      __builtin_amdgcn_sched_barrier(0);  // the reads stay a k-step ahead (see scores)
     }
 
   };
