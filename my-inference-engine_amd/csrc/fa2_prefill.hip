@@ -293,6 +293,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     rd(1, ka[1][0], ka[1][1]);
     s0 = f32x16{};
     s1 = f32x16{};
+    // The MFMA phases run at raised wave priority, so that the arbiter prefers the SIMD's MFMA
+    // stream over the other wave's softmax VALU when both are ready.
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       if (s + 2 < 8) rd(s + 2, ka[(s + 2) % 3][0], ka[(s + 2) % 3][1]);
@@ -303,6 +306,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
       // before its MFMA, which then waits the whole LDS latency.
       __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   // Online softmax of tile j's scores: P^T as the B operand (k-step kk covers keys
@@ -396,6 +400,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     };
     u32x4 va[2][4];
     rd(0, va[0]);
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       if (kk + 1 < 4) rd(kk + 1, va[(kk + 1) & 1]);
@@ -404,6 +409,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
       dma(kk);
       __builtin_amdgcn_sched_barrier(0);  // the reads stay a k-step ahead (see scores)
     }
+    __builtin_amdgcn_s_setprio(0);
 
   };
 
