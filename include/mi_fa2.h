@@ -124,6 +124,28 @@ MI_FA2_API int mi_fa2_fwd_paged(int32_t dtype, const void* q, const void* k_pool
                      mi_fa2_stream_t stream);
 
 /*
+ * Packed prefill over the paged cache: several rows, each with its own number of new query tokens,
+ * attend to their cached keys in one launch.  The reference has no counterpart: its scheduler runs
+ * one un-chunked prompt per forward (chat.py:247-253, model.py:157-199); this entry point lets a
+ * scheduler pack the prompts admitted in one step (and the single tokens of rows that only decode)
+ * into one batch.  Rows are as in mi_fa2_fwd_paged (block_table, kv_lens with this step's tokens
+ * included, bottom-right causal per row), queries packed as in mi_fa2_fwd_varlen: row b owns query
+ * tokens [cu_seqlens_q[b], cu_seqlens_q[b+1]) of q [total_q, heads_q, 128]; o like q;
+ * lse [heads_q, total_q] (may be NULL).  q/o strides: 2 (token, head); lse_strides: 2 (head, token).
+ * max_seqlen_q bounds every row's query count, max_kv_len every kv_len.  No workspace.
+ */
+MI_FA2_API int mi_fa2_fwd_paged_varlen(int32_t dtype, const void* q, const void* k_pool,
+                                       const void* v_pool, void* o, float* lse,
+                                       const int32_t* cu_seqlens_q, const int32_t* block_table,
+                                       int64_t block_table_stride, const int32_t* kv_lens,
+                                       int32_t batch, int32_t heads_q, int32_t heads_kv,
+                                       int32_t max_seqlen_q, int32_t max_kv_len, int32_t head_dim,
+                                       int32_t block_size, int32_t num_blocks,
+                                       const int64_t* q_strides, const int64_t* pool_strides,
+                                       const int64_t* o_strides, const int64_t* lse_strides,
+                                       int32_t is_causal, float sm_scale, mi_fa2_stream_t stream);
+
+/*
  * Fused rotary embedding + paged KV-cache write, the step before attention.  Replaces apply_rope
  * (model.py:62-65, applied at model.py:92) and KVCache.write (kv_cache.py:108-115, called at
  * model.py:96) on the GPU path, with bitwise the same results (the reference's 16-bit rounding

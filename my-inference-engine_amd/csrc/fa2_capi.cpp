@@ -315,6 +315,59 @@ int mi_fa2_fwd_paged(int32_t dtype, const void* q, const void* k_pool, const voi
   return launched(mi_fa2::launch_prefill(p, dtype, mi_fa2::kPaged, seqlen_q, s));
 }
 
+int mi_fa2_fwd_paged_varlen(int32_t dtype, const void* q, const void* k_pool, const void* v_pool,
+                            void* o, float* lse, const int32_t* cu_seqlens_q,
+                            const int32_t* block_table, int64_t block_table_stride,
+                            const int32_t* kv_lens, int32_t batch, int32_t heads_q,
+                            int32_t heads_kv, int32_t max_seqlen_q, int32_t max_kv_len,
+                            int32_t head_dim, int32_t block_size, int32_t num_blocks,
+                            const int64_t* q_strides, const int64_t* pool_strides,
+                            const int64_t* o_strides, const int64_t* lse_strides,
+                            int32_t is_causal, float sm_scale, mi_fa2_stream_t stream) {
+  if (int rc = check_common(dtype, batch, heads_q, heads_kv, head_dim)) return rc;
+  if (max_seqlen_q < 0 || max_kv_len < 0)
+    return fail(MI_FA2_ERR_INVALID, "bad lengths: max_seqlen_q=%d max_kv_len=%d", max_seqlen_q,
+                max_kv_len);
+  if (block_size < 16 || (block_size & (block_size - 1)))
+    return fail(MI_FA2_ERR_UNSUPPORTED, "block_size %d is not a power of two >= 16", block_size);
+  if (num_blocks < 0) return fail(MI_FA2_ERR_INVALID, "num_blocks %d < 0", num_blocks);
+  if (batch == 0 || max_seqlen_q == 0) return ok();
+  if (!cu_seqlens_q) return fail(MI_FA2_ERR_INVALID, "cu_seqlens_q is NULL");
+  if (!kv_lens) return fail(MI_FA2_ERR_INVALID, "kv_lens is NULL");
+  if (max_kv_len > 0 && !block_table) return fail(MI_FA2_ERR_INVALID, "block_table is NULL");
+  if (int rc = check_tensor("q", q, q_strides, 2)) return rc;
+  if (int rc = check_tensor("o", o, o_strides, 2)) return rc;
+  if (int rc = check_tensor("k_pool", k_pool, pool_strides, 2)) return rc;
+  if (int rc = check_tensor("v_pool", v_pool, pool_strides, 2)) return rc;
+  if (lse && !lse_strides) return fail(MI_FA2_ERR_INVALID, "lse strides are NULL");
+
+  FwdParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k_pool);
+  p.v = static_cast<const uint16_t*>(v_pool);
+  p.o = static_cast<uint16_t*>(o);
+  p.cu_q = cu_seqlens_q;
+  p.kv_lens = kv_lens;
+  p.block_table = block_table;
+  p.bt_stride = block_table_stride;
+  p.block_size = block_size;
+  p.num_blocks = num_blocks;
+  p.q_st = q_strides[0], p.q_sh = q_strides[1];
+  p.o_st = o_strides[0], p.o_sh = o_strides[1];
+  p.k_st = pool_strides[0], p.k_sh = pool_strides[1];
+  p.v_st = pool_strides[0], p.v_sh = pool_strides[1];
+  set_lse(p, lse, lse_strides, 2);
+  p.B = batch;
+  p.Hq = heads_q;
+  p.Hkv = heads_kv;
+  p.group = heads_q / heads_kv;
+  p.S = max_kv_len;
+  p.causal = is_causal ? 1 : 0;
+  p.scale_log2 = sm_scale * mi_fa2::kLog2e;
+  return launched(mi_fa2::launch_prefill(p, dtype, mi_fa2::kPagedVarlen, max_seqlen_q,
+                                         reinterpret_cast<hipStream_t>(stream)));
+}
+
 }  // extern "C"
 
 

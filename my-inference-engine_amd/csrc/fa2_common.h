@@ -34,7 +34,11 @@ constexpr float kLog2e = 1.44269504088896340736f;
 //   kDense : row b, head h, token t at base + b*s_b + h*s_h + t*s_t (the padded [B,H,S,d] layout)
 //   kVarlen: token t of row b at base + (cu_k[b] + t)*s_t + h*s_h (packed [total, H, d])
 //   kPaged : token t of row b at base + (table[b][t/bs]*bs + t%bs)*s_t + h*s_h (KVCache pool)
-enum KvMode { kDense = 0, kVarlen = 1, kPaged = 2 };
+//   kPagedVarlen: K/V as kPaged, queries packed as kVarlen ([total, H, d] + cu_q; rows of
+//            different query counts over their own cached keys)
+enum KvMode { kDense = 0, kVarlen = 1, kPaged = 2, kPagedVarlen = 3 };
+
+__host__ __device__ constexpr bool is_paged(int mode) { return mode == kPaged || mode == kPagedVarlen; }
 
 struct BF16 {
   static constexpr uint32_t kOnes2 = 0x3f803f80u;  // (1.0, 1.0)

@@ -126,6 +126,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     l_off = (int64_t)qs * p.l_st + (int64_t)h * p.l_sh;
     k_off = (int64_t)kst * p.k_st + (int64_t)hk * p.k_sh;
     v_off = (int64_t)kst * p.v_st + (int64_t)hk * p.v_sh;
+  } else if constexpr (MODE == kPagedVarlen) {
+    const int qs = p.cu_q[b];
+    T_b = p.cu_q[b + 1] - qs;
+    if (T_b < 0) T_b = 0;
+    kv_len = clamp_len(p.kv_lens[b], p.S);
+    q_off = (int64_t)qs * p.q_st + (int64_t)h * p.q_sh;
+    o_off = (int64_t)qs * p.o_st + (int64_t)h * p.o_sh;
+    l_off = (int64_t)qs * p.l_st + (int64_t)h * p.l_sh;
+    k_off = (int64_t)hk * p.k_sh;
+    v_off = (int64_t)hk * p.v_sh;
   } else {
     T_b = p.T;
     kv_len = p.kv_lens ? clamp_len(p.kv_lens[b], p.S) : p.S;
@@ -193,7 +203,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   // The offsets below are relative to the instruction's first row (paged mode) or to the tile's
   // first row (the other modes, instruction h adds 32 rows).
   const int lrow = lane >> 4;
-  const int trow = MODE == kPaged ? lrow : 4 * wave + lrow;
+  const int trow = is_paged(MODE) ? lrow : 4 * wave + lrow;
   const int k_voff = (int)(trow * p.k_st * 2) + 16 * ((lane & 15) ^ ((4 * wave + lrow) & 15));
   const int v_voff = (int)(trow * p.v_st * 2) + 16 * ((lane & 15) ^ (4 * lrow));
 
@@ -209,7 +219,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
                      int h) {
     const int i = wave + 8 * h;
     const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_base + lds_off + 1024 * i);
-    if constexpr (MODE == kPaged) {
+    if constexpr (is_paged(MODE)) {
       if (ts < 0 || ts >= kv_hi) return;
       const int r0 = ts + 4 * i;
       int n = min(max(kv_hi - r0, 0), 4);
@@ -553,10 +563,12 @@ hipError_t launch_prefill(const FwdParams& p, int dtype, int mode, int max_seqle
   if (dtype == 0) {
     if (mode == kDense) return launch_prefill_t<BF16, kDense>(p, max_seqlen_q, stream);
     if (mode == kVarlen) return launch_prefill_t<BF16, kVarlen>(p, max_seqlen_q, stream);
+    if (mode == kPagedVarlen) return launch_prefill_t<BF16, kPagedVarlen>(p, max_seqlen_q, stream);
     return launch_prefill_t<BF16, kPaged>(p, max_seqlen_q, stream);
   }
   if (mode == kDense) return launch_prefill_t<FP16, kDense>(p, max_seqlen_q, stream);
   if (mode == kVarlen) return launch_prefill_t<FP16, kVarlen>(p, max_seqlen_q, stream);
+  if (mode == kPagedVarlen) return launch_prefill_t<FP16, kPagedVarlen>(p, max_seqlen_q, stream);
   return launch_prefill_t<FP16, kPaged>(p, max_seqlen_q, stream);
 }
 

@@ -211,3 +211,52 @@ def fa2_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, is_causal=Fals
             int(max_seqlen_q), d, _strides(q), _strides(k), _strides(v), _strides(O),
             _strides(L), int(bool(is_causal)), 1.0 / math.sqrt(d), _lib.stream_of(q)))
     return (O, L) if return_lse else O
+
+
+def fa2_paged_varlen(q, k_pool, v_pool, cu_seqlens_q, block_table, kv_lens, max_seqlen_q, *,
+                     block_size=16, max_kv_len=None, is_causal=True, out=None, return_lse=False):
+    """Packed prefill of several rows over the paged cache, one launch.
+
+    q            [total_q, Hq, 128]: row b's new queries are q[cu_q[b]:cu_q[b+1]] (rows may have
+                 different counts, 0 included)
+    k_pool/v_pool, block_table, kv_lens, block_size, max_kv_len: as in fa2_paged; kv_lens include
+                 each row's new tokens, whose K/V are already in the pool
+    is_causal    bottom-right aligned per row (query i of row b sees keys <= i + kv_len - T_b)
+    out          optional [total_q, Hq, 128] output (any token/head strides)
+    Returns O [total_q, Hq, 128] (and the fp32 LSE [Hq, total_q] if return_lse).
+    """
+    assert q.is_cuda and k_pool.is_cuda and v_pool.is_cuda, "q and the pools must be GPU tensors"
+    assert q.dim() == 3, "q is [total_q, Hq, d]"
+    total_q, Hq, d = q.shape
+    B = cu_seqlens_q.shape[0] - 1
+    assert k_pool.dim() == 3 and k_pool.shape == v_pool.shape, "pools are [slots, Hkv, d]"
+    assert k_pool.stride() == v_pool.stride(), "k_pool and v_pool must share strides"
+    Hkv = k_pool.shape[1]
+    assert Hq % Hkv == 0, "query heads must be a multiple of kv heads (GQA)"
+    assert cu_seqlens_q.dtype == torch.int32 and kv_lens.dtype == torch.int32
+    assert kv_lens.shape == (B,)
+    assert block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == B
+    assert block_table.stride(-1) == 1, "block_table rows must be contiguous"
+    assert block_size >= 16 and block_size & (block_size - 1) == 0, "block_size: power of 2, >= 16"
+    assert k_pool.shape[0] % block_size == 0, "pool slots must be whole blocks"
+    _envelope(q, k_pool, v_pool)
+    if max_kv_len is None:
+        max_kv_len = block_table.shape[1] * block_size
+    assert 0 <= max_kv_len <= block_table.shape[1] * block_size, \
+        "max_kv_len exceeds what the block table can address"
+    q = _vec(q)
+    assert _dims_ok(k_pool) and _dims_ok(v_pool), "pools need 16-byte aligned token rows"
+    O = out if out is not None else torch.empty((total_q, Hq, d), device=q.device, dtype=q.dtype)
+    assert O.shape == q.shape and O.dtype == q.dtype and _dims_ok(O)
+    L = torch.empty((Hq, total_q), device=q.device, dtype=torch.float32) if return_lse else None
+    lib = _lib.load()
+    pool_strides = (_lib.ctypes.c_int64 * 2)(*k_pool.stride()[:2])
+    with torch.cuda.device(q.device):
+        _lib.check(lib.mi_fa2_fwd_paged_varlen(
+            _lib.DTYPES[q.dtype], q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), O.data_ptr(),
+            L.data_ptr() if L is not None else None, cu_seqlens_q.data_ptr(),
+            block_table.data_ptr(), block_table.stride(0), kv_lens.data_ptr(), B, Hq, Hkv,
+            int(max_seqlen_q), int(max_kv_len), d, block_size, k_pool.shape[0] // block_size,
+            _strides(q), pool_strides, _strides(O), _strides(L) if L is not None else None,
+            int(bool(is_causal)), 1.0 / math.sqrt(d), _lib.stream_of(q)))
+    return (O, L) if return_lse else O

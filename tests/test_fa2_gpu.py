@@ -223,6 +223,42 @@ def test_paged_prefill_over_cached_context():
     check_close(out, _paged_ref(q, kp, vp, tables, lens, bs, True), what="paged prefill")
 
 
+def test_paged_varlen_mixed_rows():
+    # One packed launch over rows with different new-token counts (a prompt, decode rows of one
+    # token, an empty row, a row whose new tokens are all its keys), each against its own cached
+    # keys through its block table; unused pool slots hold NaN, which must never be read.
+    from kernels.fa2 import fa2_paged_varlen
+    g = torch.Generator().manual_seed(11)
+    Ts = [37, 1, 200, 0, 1, 129]
+    lens = [100, 513, 200, 40, 1, 300]
+    bs, num_blocks = 16, 128
+    tables = opaged.random_tables(lens, bs, num_blocks, g)
+    kp = torch.full((num_blocks * bs, 2, 128), float("nan")).to(torch.bfloat16)
+    vp = torch.full((num_blocks * bs, 2, 128), float("nan")).to(torch.bfloat16)
+    for b, n in enumerate(lens):
+        for t in range(n):
+            slot = tables[b][t // bs] * bs + t % bs
+            kp[slot] = torch.randn(2, 128, generator=g).to(torch.bfloat16)
+            vp[slot] = torch.randn(2, 128, generator=g).to(torch.bfloat16)
+    cu = [0]
+    for t in Ts:
+        cu.append(cu[-1] + t)
+    q = torch.randn(cu[-1], 12, 128, generator=g).to(torch.bfloat16)
+    announce("[gpu] paged varlen mixed rows")
+    out = fa2_paged_varlen(q.to(DEV), kp.to(DEV), vp.to(DEV),
+                           torch.tensor(cu, dtype=torch.int32, device=DEV),
+                           wl.table_tensor(tables).to(DEV),
+                           torch.tensor(lens, dtype=torch.int32, device=DEV), max(Ts))
+    torch.cuda.synchronize()
+    for b, T in enumerate(Ts):
+        if T == 0:
+            continue
+        qb = q[cu[b]:cu[b + 1]].transpose(0, 1).unsqueeze(0)  # [1, Hq, T, d]
+        ref = _paged_ref(qb, kp, vp, [tables[b]], [lens[b]], bs, True)
+        check_close(out[cu[b]:cu[b + 1]].transpose(0, 1).unsqueeze(0), ref,
+                    what=f"paged varlen row {b} (T={T}, kv_len={lens[b]})")
+
+
 def test_paged_block_size_32():
     g = torch.Generator().manual_seed(6)
     lens, bs = [33, 700, 64], 32
