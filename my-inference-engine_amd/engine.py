@@ -16,6 +16,12 @@ globals and a daemon worker thread:
   * a finished reply keeps its cache (the conversation continues), appends the separator and
     gives back reserved-but-unused blocks (chat.py:194-211).
 
+With mixed_prefill=True the admission rules stay, but an admitted prompt no longer runs a forward
+of its own: its tokens join the tick's decode step as one more row of a packed mixed batch
+(Qwen2ForCausalLM.forward_mixed), and its first reply token is sampled with the decode rows.  Then
+several prompts may be admitted per tick, up to max_step_tokens prompt tokens (one prompt is always
+admitted, however long, as the reference's un-chunked prefill is).
+
 Tokenizer, stop sequences, streaming listeners and the web UI are outside the attention path and
 not rebuilt; conversations carry token ids.
 """
@@ -45,12 +51,15 @@ class Job:
     t_first: float = None
     t_done: float = None
     rejected: str = None
+    prefill: list = None   # mixed mode: prompt tokens waiting for the next step
 
 
 class Engine:
     def __init__(self, model, cache, *, max_reply_tokens=512, temperature=1.0, sep_ids=(198,),
-                 seed=0, decode_graphs=None):
+                 seed=0, decode_graphs=None, mixed_prefill=False, max_step_tokens=16384):
         self.model = model
+        self.mixed_prefill = mixed_prefill
+        self.max_step_tokens = max_step_tokens
         self.cache = cache
         self.decode_graphs = decode_graphs  # graphs.DecodeGraphs, or None: eager decode steps
         self.max_reply_tokens = max_reply_tokens
@@ -81,6 +90,8 @@ class Engine:
 
     def tick(self):
         """One worker iteration (chat.py:232-254)."""
+        if self.mixed_prefill:
+            return self._tick_mixed()
         for job in list(self.deferred):
             if self._make_room(job):
                 self.deferred.remove(job)
@@ -92,6 +103,36 @@ class Engine:
             pass  # deferred jobs wait for blocks to be released (the reference sleeps)
         elif self.queue:
             self._try_admit_or_defer(self.queue.popleft())
+        self._process()
+
+    def _tick_mixed(self):
+        """Admissions fill the step's prompt-token budget; deferred jobs go first, then the queue
+        until a job has to wait.  With nothing active and jobs deferred, new ones wait too (the
+        reference sleeps there)."""
+        budget = [self.max_step_tokens]
+
+        def fits(job):
+            n = len(job.conv.ids) + len(job.new_ids) - (
+                self.cache.length(job.conv.seq) if job.conv.seq is not None else 0)
+            return n <= budget[0] or not any(j.prefill is not None for j in self.active)
+
+        def admit(job):
+            self._admit(job)
+            budget[0] -= len(job.prefill)
+
+        for job in list(self.deferred):
+            if fits(job) and self._make_room(job):
+                self.deferred.remove(job)
+                admit(job)
+        if self.active or not self.deferred:
+            while self.queue and fits(self.queue[0]):
+                job = self.queue.popleft()
+                before = len(self.deferred)
+                self._try_admit_or_defer(job)
+                if job in self.active:
+                    budget[0] -= len(job.prefill)
+                elif len(self.deferred) > before:
+                    break
         self._process()
 
     def run_until_idle(self, max_ticks=1_000_000):
@@ -154,6 +195,10 @@ class Engine:
         prefill = conv.ids[self.cache.length(conv.seq):]
         self.cache.ensure_capacity(conv.seq, reserve)
         self._touch(conv)
+        if self.mixed_prefill:
+            job.prefill = prefill     # runs inside the next step, as one more row
+            self.active.append(job)
+            return
         input_ids = torch.tensor([prefill], device=self.device)
         with torch.no_grad():
             logits = self.model(input_ids, self.cache, [conv.seq])
@@ -171,8 +216,11 @@ class Engine:
         self.finished.append(job)
 
     def _process(self):
-        continuing = []
+        continuing, prompts = [], []
         for job in list(self.active):
+            if job.prefill is not None:
+                prompts.append(job)
+                continue
             tok = job.next_token
             job.conv.ids.append(tok)
             job.generated.append(tok)
@@ -184,6 +232,8 @@ class Engine:
                 self._finish(job)
                 continue
             continuing.append(job)
+        if prompts:
+            return self._step_mixed(continuing, prompts)
         if not continuing:
             return
         seqs = [j.conv.seq for j in continuing]
@@ -196,6 +246,20 @@ class Engine:
                 last = self.model(input_ids, self.cache, seqs)[:, -1]
         for job, tok in zip(continuing, self._sample(last)):
             job.next_token = tok
+
+    def _step_mixed(self, continuing, prompts):
+        """One packed step: the decode rows first (one token each), then the admitted prompts."""
+        jobs = continuing + prompts
+        rows = [[j.next_token] for j in continuing] + [j.prefill for j in prompts]
+        with torch.no_grad():
+            logits = self.model.forward_mixed(rows, self.cache, [j.conv.seq for j in jobs])
+        toks = self._sample(logits)
+        now = time.perf_counter()
+        for job, tok in zip(jobs, toks):
+            job.next_token = tok
+        for job in prompts:
+            job.prefill = None
+            job.t_first = now
 
     def _sample(self, logits):
         """One id per row of [B, vocab] logits, one device sync for all rows (chat.py:103-107)."""

@@ -133,7 +133,7 @@ class _Ctx:
 
 
 def fa2_paged(q, k_pool, v_pool, block_table, kv_lens, *, block_size=16, max_kv_len=None,
-              is_causal=None, return_lse=False):
+              is_causal=None, out=None, return_lse=False):
     """Attention over K/V held in a paged pool, read in-kernel through a block table.
 
     q            [B, Hq, T, 128]   this step's queries (T = 1 for decode)
@@ -143,6 +143,7 @@ def fa2_paged(q, k_pool, v_pool, block_table, kv_lens, *, block_size=16, max_kv_
     kv_lens      [B] int32: keys per row including this step's T (model.py:175)
     max_kv_len   host-side upper bound of kv_lens (default W * block_size)
     is_causal    default T > 1, as model.py:185 sets it; bottom-right aligned per row
+    out          optional [B, Hq, T, 128] output (any row/head/token strides, 16-byte aligned)
     Returns O [B, Hq, T, 128] (and the fp32 LSE [B, Hq, T] if return_lse).
     """
     assert q.is_cuda and k_pool.is_cuda and v_pool.is_cuda, "q and the pools must be GPU tensors"
@@ -166,7 +167,8 @@ def fa2_paged(q, k_pool, v_pool, block_table, kv_lens, *, block_size=16, max_kv_
         is_causal = T > 1
     q = _vec(q)
     assert _dims_ok(k_pool) and _dims_ok(v_pool), "pools need 16-byte aligned token rows"
-    O = torch.empty((B, Hq, T, d), device=q.device, dtype=q.dtype)
+    O = out if out is not None else torch.empty((B, Hq, T, d), device=q.device, dtype=q.dtype)
+    assert O.shape == q.shape and O.dtype == q.dtype and _dims_ok(O)
     L = torch.empty((B, Hq, T), device=q.device, dtype=torch.float32)
     lib = _lib.load()
     nbytes = lib.mi_fa2_fwd_paged_workspace_size(B, Hq, Hkv, T, max_kv_len, d)

@@ -18,6 +18,11 @@ numpy and ONE pinned host-to-device copy, exactly what the paged kernel reads:
 
 and no per-layer gather happens on the GPU path.  read() (the dense gather) is kept for the CPU
 fallback and for reference-compatible callers.
+
+prepare_packed() builds the metadata of a mixed step, where each row appends its own number of
+tokens (one for a decoding chat, a whole prompt for a newly admitted one) and the rows' tokens are
+packed back to back: prefix offsets cu_q, every token's position and slot, and each row's last
+token (whose logits are sampled).
 """
 import math
 from dataclasses import dataclass, field
@@ -39,6 +44,7 @@ class StepMeta:
     slot_mapping32: torch.Tensor = None  # the same slots as int32 (for the fused RoPE + write)
     tables: list = field(default_factory=list)  # host copies of the rows' block lists
     kv_cap: int = None           # fixed upper bound of kv_lens (captured decode graphs)
+    packed = False
 
     @property
     def max_kv(self):
@@ -58,6 +64,43 @@ class StepMeta:
         starts = torch.tensor(self.starts, device=device)
         q_pos = starts[:, None] + torch.arange(self.T, device=device)[None, :]
         return (key_pos[None, None, :] <= q_pos[:, :, None]).unsqueeze(1)
+
+
+@dataclass
+class PackedMeta:
+    """Metadata of one mixed step: row b appends counts[b] >= 1 tokens, packed back to back in row
+    order (row b's tokens are [cu_q[b], cu_q[b+1]) of the packed batch)."""
+    starts: list                 # tokens each row held before this step (host ints)
+    counts: list                 # new tokens per row (host ints)
+    block_size: int
+    n_single: int                # leading rows with exactly one new token (decode-shaped rows)
+    cu_q: torch.Tensor           # [B+1] int32
+    kv_lens: torch.Tensor        # [B] int32 = starts + counts
+    positions: torch.Tensor      # [N] int32: position of each packed token in its row
+    slot_mapping32: torch.Tensor  # [N] int32: cache slot of each packed token
+    last_idx: torch.Tensor       # [B] int32: packed index of each row's last token
+    block_table: torch.Tensor    # [B, W] int32
+    tables: list = field(default_factory=list)
+    packed = True
+
+    def split(self):
+        """(max kv_len of the leading one-token rows, of the other rows, max new tokens of the
+        other rows): the host bounds each attention launch is sized by."""
+        D = self.n_single
+        kv = [s + c for s, c in zip(self.starts, self.counts)]
+        return (max(kv[:D], default=0), max(kv[D:], default=0), max(self.counts[D:], default=0))
+
+    @property
+    def max_kv(self):
+        return max(s + c for s, c in zip(self.starts, self.counts))
+
+    @property
+    def max_q(self):
+        return max(self.counts)
+
+    @property
+    def slot_mapping(self):
+        return self.slot_mapping32.long()
 
 
 class KVCache:
@@ -110,8 +153,10 @@ class KVCache:
         del table[keep:]
 
     def advance(self, seqs, T):
-        for s in seqs:
-            self._lengths[s] += T
+        """Count T new tokens (an int, or one count per row) as written."""
+        counts = T if isinstance(T, (list, tuple)) else [T] * len(seqs)
+        for s, c in zip(seqs, counts):
+            self._lengths[s] += c
 
     # -- per-step metadata ----------------------------------------------------------------------
     def pack_step(self, seqs, T, W=None, out=None, rows=None):
@@ -162,6 +207,48 @@ class KVCache:
             slot_mapping32=dev[2 * B + B * W:],
             tables=[list(t) for t in tables])
 
+    def prepare_packed(self, seqs, counts):
+        """Grow the rows' tables for counts[b] new tokens each and build a PackedMeta with one
+        pinned host-to-device copy of [cu_q | kv_lens | positions | slots | last_idx | tables]."""
+        assert len(seqs) == len(counts) and len(seqs) > 0 and min(counts) >= 1
+        bs = self.block_size
+        starts = [self._lengths[s] for s in seqs]
+        for s, start, c in zip(seqs, starts, counts):
+            self.ensure_capacity(s, start + c)
+        B, N = len(seqs), sum(counts)
+        st = np.asarray(starts, dtype=np.int32)
+        cnt = np.asarray(counts, dtype=np.int32)
+        kv = st + cnt
+        W = max(1, math.ceil(int(kv.max()) / bs))
+        tables = [self._block_tables[s] for s in seqs]
+        host = np.zeros(2 * B + 1 + 2 * N + B + B * W, dtype=np.int32)
+        cu = host[:B + 1]
+        np.cumsum(cnt, out=cu[1:])
+        host[B + 1:2 * B + 1] = kv
+        o = 2 * B + 1
+        row = np.repeat(np.arange(B), cnt)                          # row of each packed token
+        pos = host[o:o + N]
+        pos[:] = st[row] + (np.arange(N, dtype=np.int32) - cu[:-1][row])
+        bt = host[o + 2 * N + B:].reshape(B, W)
+        for i, t in enumerate(tables):
+            n = min(len(t), W)
+            bt[i, :n] = t[:n]
+        host[o + N:o + 2 * N] = bt[row, pos // bs] * bs + pos % bs
+        host[o + 2 * N:o + 2 * N + B] = cu[1:] - 1
+        n_single = 0
+        while n_single < B and counts[n_single] == 1:
+            n_single += 1
+        cpu = torch.from_numpy(host)
+        if self.device.type == "cuda":
+            dev = cpu.pin_memory().to(self.device, non_blocking=True)
+        else:
+            dev = cpu.clone()
+        return PackedMeta(
+            starts=starts, counts=list(counts), block_size=bs, n_single=n_single,
+            cu_q=dev[:B + 1], kv_lens=dev[B + 1:2 * B + 1], positions=dev[o:o + N],
+            slot_mapping32=dev[o + N:o + 2 * N], last_idx=dev[o + 2 * N:o + 2 * N + B],
+            block_table=dev[o + 2 * N + B:].view(B, W), tables=[list(t) for t in tables])
+
     # -- data movement --------------------------------------------------------------------------
     def k_pool(self, layer):
         return self.buf[layer, 0]
@@ -174,6 +261,14 @@ class KVCache:
         B, H, T, D = k.shape
         self.buf[layer, 0].index_copy_(0, meta.slot_mapping, k.transpose(1, 2).reshape(B * T, H, D))
         self.buf[layer, 1].index_copy_(0, meta.slot_mapping, v.transpose(1, 2).reshape(B * T, H, D))
+
+    def read_row(self, layer, table, n):
+        """Dense [Hkv, n, d] copies of the first n keys/values of the sequence whose block list is
+        `table`: one row of read()."""
+        pos = torch.arange(n, device=self.buf.device)
+        idx = torch.tensor(table, device=self.buf.device, dtype=torch.long)[pos // self.block_size]
+        idx = idx * self.block_size + pos % self.block_size
+        return self.buf[layer, 0][idx].transpose(0, 1), self.buf[layer, 1][idx].transpose(0, 1)
 
     def read(self, layer, meta):
         """Dense [B, Hkv, S, d] copies of every row's keys/values (kv_cache.py:117-121)."""

@@ -12,6 +12,13 @@ logits (model.py:204-207) -- with two deliberate differences on the GPU path:
   * RoPE and the cache write are one HIP launch (kernels.rope.rope_kv_write) instead of the
     elementwise RoPE ops and two index_copy_ (model.py:92,96), with bitwise the same results.
 
+forward_mixed() runs one step over rows that append different numbers of tokens -- decoding chats
+(one token each) and newly admitted prompts -- packed back to back: every projection, norm and MLP
+runs once over all packed tokens, attention goes to the paged decode kernel for the leading
+one-token rows and to the paged varlen prefill kernel for the prompt rows, and only each row's last
+token reaches the logits.  The reference runs each admitted prompt as a forward of its own
+(chat.py:157-185, one per tick, chat.py:247-253) beside the batched decode step.
+
 On CPU tensors the model takes the reference's own fallback (dense read + fp32 SDPA with the
 bottom-right mask, model.py:104-107,181-195), which only the CPU tests of the scheduler use; the
 attention kernels themselves have no CPU path.
@@ -22,7 +29,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from kernels.fa2 import fa2_paged
+from kernels.fa2 import fa2_paged, fa2_paged_varlen
 from kernels.rope import rope_kv_write
 
 
@@ -92,6 +99,10 @@ class Attention(nn.Module):
                               sin[:, 0].reshape(B * T, cfg.head_dim), meta.slot_mapping32,
                               cache.k_pool(layer), cache.v_pool(layer), cfg.num_heads,
                               cfg.num_kv_heads)
+            if meta.packed:
+                out = self._attend_packed(q.view(B * T, cfg.num_heads, cfg.head_dim), cache,
+                                          layer, meta)
+                return self.o_proj(out.view(B, T, self.q_size))
             q = q.view(B, T, cfg.num_heads, cfg.head_dim).transpose(1, 2)
             out = fa2_paged(q, cache.k_pool(layer), cache.v_pool(layer), meta.block_table,
                             meta.kv_lens, block_size=cache.block_size, max_kv_len=meta.max_kv,
@@ -103,11 +114,45 @@ class Attention(nn.Module):
             v = v.view(B, T, cfg.num_kv_heads, cfg.head_dim).transpose(1, 2)
             q, k = apply_rope(q, k, cos, sin)
             cache.write(layer, meta, k, v)
+            if meta.packed:
+                out = self._attend_packed_cpu(q, cache, layer, meta)
+                return self.o_proj(out.transpose(1, 2).reshape(B, T, self.q_size))
             k_all, v_all = cache.read(layer, meta)
             n_rep = cfg.num_heads // cfg.num_kv_heads
             out = F.scaled_dot_product_attention(q, repeat_kv(k_all, n_rep), repeat_kv(v_all, n_rep),
                                                  attn_mask=meta.dense_mask(x.device))
         return self.o_proj(out.transpose(1, 2).reshape(B, T, self.q_size))
+
+    def _attend_packed(self, q, cache, layer, meta):
+        """q [N, Hq, d] packed queries of a mixed step -> [N, Hq, d]: the leading one-token rows
+        through the paged decode kernel, the rest through the paged varlen prefill kernel, both
+        writing into one packed output."""
+        out = torch.empty_like(q)
+        D, B, bs = meta.n_single, len(meta.counts), cache.block_size
+        kv_single, kv_multi, q_multi = meta.split()
+        kp, vp = cache.k_pool(layer), cache.v_pool(layer)
+        if D:
+            fa2_paged(q[:D].unsqueeze(2), kp, vp, meta.block_table[:D], meta.kv_lens[:D],
+                      block_size=bs, max_kv_len=kv_single, is_causal=False,
+                      out=out[:D].unsqueeze(2))
+        if D < B:
+            fa2_paged_varlen(q, kp, vp, meta.cu_q[D:], meta.block_table[D:], meta.kv_lens[D:],
+                             q_multi, block_size=bs, max_kv_len=kv_multi, is_causal=True, out=out)
+        return out
+
+    def _attend_packed_cpu(self, q, cache, layer, meta):
+        """The dense fallback row by row: q [1, Hq, N, d] -> [1, Hq, N, d] (model.py:181-195)."""
+        n_rep = self.cfg.num_heads // self.cfg.num_kv_heads
+        outs, c0 = [], 0
+        for start, count, table in zip(meta.starts, meta.counts, meta.tables):
+            k_all, v_all = cache.read_row(layer, table, start + count)
+            mask = (torch.arange(start + count, device=q.device)[None, :]
+                    <= start + torch.arange(count, device=q.device)[:, None])
+            outs.append(F.scaled_dot_product_attention(
+                q[:, :, c0:c0 + count], repeat_kv(k_all[None], n_rep), repeat_kv(v_all[None], n_rep),
+                attn_mask=mask))
+            c0 += count
+        return torch.cat(outs, dim=2)
 
 
 class MLP(nn.Module):
@@ -182,4 +227,26 @@ class Qwen2ForCausalLM(nn.Module):
         for layer_idx, layer in enumerate(self.layers):
             x = layer(x, cos, sin, cache, layer_idx, meta)
         x = self.norm(x[:, -1:])
+        return x @ self.embed_tokens.weight.T
+
+    def forward_mixed(self, rows, cache, seqs):
+        """One packed step: rows[b] (a list of token ids, at least one) is appended to cache
+        sequence seqs[b].  Returns each row's last-token logits [B, vocab]."""
+        counts = [len(r) for r in rows]
+        meta = cache.prepare_packed(seqs, counts)
+        ids = torch.tensor([t for r in rows for t in r], dtype=torch.long)
+        if cache.device.type == "cuda":
+            ids = ids.pin_memory().to(cache.device, non_blocking=True)
+        logits = self.forward_packed(ids, cache, meta)
+        cache.advance(seqs, counts)
+        return logits
+
+    def forward_packed(self, token_ids, cache, meta):
+        """The layers over a prepared mixed step (KVCache.prepare_packed): token_ids [N] are the
+        rows' new tokens back to back; returns the rows' last-token logits [B, vocab]."""
+        x = self.embed_tokens(token_ids)[None]                      # [1, N, hidden]
+        cos, sin = self.rope_cos_sin(meta.positions[None], x.dtype)
+        for layer_idx, layer in enumerate(self.layers):
+            x = layer(x, cos, sin, cache, layer_idx, meta)
+        x = self.norm(x[0, meta.last_idx.long()])
         return x @ self.embed_tokens.weight.T

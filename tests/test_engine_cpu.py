@@ -151,3 +151,113 @@ def test_trim_returns_unused_reserved_blocks():
     job.max_tokens = 2  # end early
     eng.run_until_idle()
     assert len(eng.cache._block_tables[conv.seq]) == math.ceil(eng.cache.length(conv.seq) / 16)
+
+
+# -- mixed prefill + decode steps ----------------------------------------------------------------
+
+def test_prepare_packed_metadata_matches_slot_arithmetic():
+    cache = tiny_cache(num_blocks=40)
+    seqs = [cache.alloc() for _ in range(4)]
+    for s, n in zip(seqs, (37, 16, 0, 5)):
+        cache.ensure_capacity(s, n)
+        cache._lengths[s] = n
+    counts = [1, 1, 20, 3]
+    meta = cache.prepare_packed(seqs, counts)
+    assert meta.n_single == 2 and meta.starts == [37, 16, 0, 5]
+    assert meta.cu_q.tolist() == [0, 1, 2, 22, 25]
+    assert meta.kv_lens.tolist() == [38, 17, 20, 8]
+    assert meta.last_idx.tolist() == [0, 1, 21, 24]
+    assert meta.split() == (38, 20, 20)
+    pos, slots = meta.positions.tolist(), meta.slot_mapping32.tolist()
+    i = 0
+    for b, s in enumerate(seqs):
+        table = cache._block_tables[s]
+        assert meta.block_table[b, :len(table)].tolist() == table[:meta.block_table.shape[1]]
+        for t in range(counts[b]):
+            assert pos[i] == meta.starts[b] + t
+            assert slots[i] == opaged.slot_of(table, pos[i], 16)
+            i += 1
+    assert i == 25
+
+
+def test_mixed_step_equals_separate_forwards():
+    """Decode rows and new prompts packed into one step give each row the logits of running it on
+    its own, and each row's cache length grows by its own count."""
+    model = tiny_model(2)
+    g = torch.Generator().manual_seed(5)
+    hist = [torch.randint(0, TINY.vocab_size, (n,), generator=g).tolist() for n in (9, 40, 17)]
+    nxt = torch.randint(0, TINY.vocab_size, (3,), generator=g).tolist()
+    new = [torch.randint(0, TINY.vocab_size, (n,), generator=g).tolist() for n in (30, 1, 12)]
+    with torch.no_grad():
+        mc = tiny_cache()
+        mseqs = [mc.alloc() for _ in range(6)]
+        for s, h in zip(mseqs, hist):
+            model(torch.tensor([h]), mc, [s])
+        # rows 0-2 decode one token, rows 3-5 are prompts (one of them a single token)
+        got = model.forward_mixed([[t] for t in nxt] + new, mc, mseqs)
+        want = []
+        for rows in [h + [t] for h, t in zip(hist, nxt)] + new:
+            c = tiny_cache()
+            s = c.alloc()
+            want.append(model(torch.tensor([rows]), c, [s])[:, -1])
+    assert torch.allclose(got, torch.cat(want), atol=1e-5, rtol=1e-4)
+    assert [mc.length(s) for s in mseqs] == [10, 41, 18, 30, 1, 12]
+
+
+def _mixed_engine(num_blocks, reply=4, **kw):
+    return Engine(tiny_model(), tiny_cache(num_blocks=num_blocks), max_reply_tokens=reply, seed=0,
+                  mixed_prefill=True, **kw)
+
+
+def test_mixed_engine_admits_every_prompt_into_one_step():
+    eng = _mixed_engine(64)
+    g = torch.Generator().manual_seed(3)
+    prompts = [torch.randint(0, TINY.vocab_size, (n,), generator=g).tolist() for n in (7, 40, 3, 21)]
+    jobs = [eng.submit(Conversation(), p, 4) for p in prompts]
+    eng.tick()
+    assert len(eng.active) == 4 and all(j.t_first is not None and j.prefill is None for j in jobs)
+    eng.run_until_idle()
+    assert all(len(j.generated) == 4 for j in jobs)
+    for j in jobs:
+        eng.release(j.conv)
+    assert eng.cache.free_block_count() == 64
+
+
+def test_mixed_engine_respects_the_step_token_budget():
+    eng = _mixed_engine(64, max_step_tokens=50)
+    jobs = [eng.submit(Conversation(), list(range(n)), 4) for n in (30, 30, 60, 10)]
+    eng.tick()   # 30 fits, the second 30 would pass 50: one admission
+    assert [j in eng.active for j in jobs] == [True, False, False, False]
+    eng.tick()   # a step with decode rows only still has the whole budget: 30, then 60 waits
+    assert [j in eng.active for j in jobs] == [True, True, False, False]
+    eng.tick()   # 60 > 50 but it is the step's first prompt: admitted alone (un-chunked)
+    assert [j in eng.active for j in jobs] == [True, True, True, False]
+    eng.run_until_idle()
+    assert all(len(j.generated) == 4 for j in jobs)
+
+
+def test_mixed_engine_defers_and_evicts_like_the_reference():
+    eng = _mixed_engine(6)
+    convs = [Conversation() for _ in range(3)]
+    jobs = [eng.submit(c, list(range(40)), 4) for c in convs]
+    eng.tick()
+    # each job reserves 3 of the 6 blocks: two admitted in the first step, the third deferred
+    assert len(eng.active) == 2 and not eng.queue and len(eng.deferred) == 1
+    eng.run_until_idle()
+    assert all(len(j.generated) == 4 for j in jobs)
+    assert sum(c.seq is None for c in convs) >= 1
+
+
+def test_mixed_and_separate_prefill_generate_the_same_tokens():
+    """Near-greedy sampling (temperature 1e-4) makes the sampled ids a function of the logits
+    only, so the two schedules must produce the same replies."""
+    g = torch.Generator().manual_seed(7)
+    prompts = [torch.randint(0, TINY.vocab_size, (n,), generator=g).tolist() for n in (7, 40, 3, 21, 16)]
+    replies = []
+    for mixed in (False, True):
+        eng = Engine(tiny_model(), tiny_cache(num_blocks=64), max_reply_tokens=6, seed=0,
+                     temperature=1e-4, mixed_prefill=mixed)
+        jobs = [eng.submit(Conversation(), p, 6) for p in prompts]
+        eng.run_until_idle()
+        replies.append([j.generated for j in jobs])
+    assert replies[0] == replies[1]

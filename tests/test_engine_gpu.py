@@ -104,3 +104,53 @@ def test_engine_with_decode_graphs_completes():
     summary = run_concurrent_chats(eng, prompts, reply_tokens=8)
     assert summary["tokens"] == 32
     assert cache.free_block_count() == 128
+
+
+def test_gpu_mixed_step_matches_separate_steps():
+    """A packed step (3 decode rows, then prompts of 150, 1 and 40 tokens: the 1-token prompt
+    goes through the varlen prefill kernel, not the decode kernel) against the unpacked GPU
+    forwards and the CPU fp32 model with the same weights."""
+    g = torch.Generator().manual_seed(6)
+    hist = [torch.randint(0, SMALL.vocab_size, (n,), generator=g).tolist() for n in (37, 200, 5)]
+    nxt = torch.randint(0, SMALL.vocab_size, (3,), generator=g).tolist()
+    new = [torch.randint(0, SMALL.vocab_size, (n,), generator=g).tolist() for n in (150, 1, 40)]
+    gm, gc = make("cuda", torch.bfloat16)
+    cm, cc = make("cpu", torch.float32)
+    cm.load_state_dict({k: v.float().cpu() for k, v in gm.state_dict().items()})
+    rows = [[t] for t in nxt] + new
+    got = {}
+    for model, cache, dev in ((gm, gc, "cuda"), (cm, cc, "cpu")):
+        seqs = [cache.alloc() for _ in range(6)]
+        announce(f"[gpu] mixed step on {dev}: decode rows 3, prompts (150, 1, 40)")
+        with torch.no_grad():
+            for s, h in zip(seqs, hist):
+                model(torch.tensor([h], device=dev), cache, [s])
+            got[dev] = model.forward_mixed(rows, cache, seqs).float().cpu()
+        assert [cache.length(s) for s in seqs] == [38, 201, 6, 150, 1, 40]
+    announce("[gpu] mixed step: unpacked GPU forwards")
+    want = []
+    with torch.no_grad():
+        for r in [h + [t] for h, t in zip(hist, nxt)] + new:
+            m2, c2 = gm, KVCache(64, 16, "cuda", torch.bfloat16, SMALL.num_layers,
+                                 SMALL.num_kv_heads, SMALL.head_dim)
+            want.append(m2(torch.tensor([r], device="cuda"), c2, [c2.alloc()])[:, -1].float().cpu())
+    torch.cuda.synchronize()
+    want = torch.cat(want)
+    gpu, cpu = got["cuda"], got["cpu"]
+    scale = cpu.abs().max().item()
+    assert (gpu - want).abs().max().item() <= 0.02 * scale
+    cos = torch.nn.functional.cosine_similarity(gpu.flatten(), cpu.flatten(), dim=0).item()
+    assert cos > 0.999 and (gpu - cpu).abs().max().item() <= 0.05 * scale, cos
+
+
+def test_engine_mixed_prefill_with_decode_graphs_completes():
+    from graphs import DecodeGraphs
+    model, cache = make("cuda", torch.bfloat16, num_blocks=128)
+    graphs = DecodeGraphs(model, cache, buckets=(1, 2, 4))
+    eng = Engine(model, cache, max_reply_tokens=8, seed=0, decode_graphs=graphs, mixed_prefill=True)
+    g = torch.Generator().manual_seed(4)
+    prompts = [torch.randint(0, SMALL.vocab_size, (n,), generator=g).tolist() for n in (40, 7, 300, 96)]
+    announce("[gpu] 4 concurrent chats x 8 tokens, mixed prefill steps + decode graphs")
+    summary = run_concurrent_chats(eng, prompts, reply_tokens=8)
+    assert summary["tokens"] == 32
+    assert cache.free_block_count() == 128
