@@ -163,7 +163,7 @@ def e2e_line(e2e):
                 "tpot_s": round(r["tpot"], 5)}
     rec = {"metric": "e2e tok/s at 16 chats", "value": round(m["tok_per_s"], 1), "unit": "tok/s",
            "tokens": m["tokens"], "schedule": "mixed prefill+decode steps, decode-only steps "
-           "replayed as HIP graphs"}
+           "replayed as HIP graphs, tokens drawn by the fused HIP sampler"}
     rec.update(figs(m))
     rec["separate_prefill"] = figs(s)
     rec["workload"] = (f"Qwen2.5-1.5B architecture, random N(0,0.02) bf16 weights; 16 chats, "

@@ -6,13 +6,15 @@
  *   - its launcher `FlashAttention2Function`     (kernels/fa2.py:164-214),
  *   - the per-step dense K/V gather it is fed by (kv_cache.py:117-121, called at model.py:97),
  * with hand-written HIP kernels: an MFMA/LDS-tiled prefill kernel, a split-KV decode kernel that
- * reads K/V straight out of the paged cache's blocks, and a split combine kernel.
+ * reads K/V straight out of the paged cache's blocks, and a split combine kernel; and the steps
+ * either side of it: a fused RoPE + paged cache write and a fused last-position token sampler.
  *
  * Conventions shared by every entry point
  *   - All pointers are device pointers except the stride arrays, which are host arrays.
  *   - Strides are in ELEMENTS, int64.  The innermost (head_dim) stride must be 1, every other stride
  *     a multiple of 8 elements and every tensor base 16-byte aligned (16-byte vector loads).
- *   - `dtype` is MI_FA2_BF16 or MI_FA2_FP16; q, k, v and o share it.  Softmax and accumulation
+ *   - `dtype` is MI_FA2_BF16 or MI_FA2_FP16; q, k, v and o share it (the sampler also takes
+ *     MI_FA2_FP32 logits).  Softmax and accumulation
  *     are fp32; `lse` is fp32 (natural log, like the reference's L, kernels/fa2.py:158,189).
  *   - head_dim must be 128 (the Qwen2.5 shape); heads_q must be a multiple of heads_kv and query
  *     head h reads kv head h / (heads_q / heads_kv) (kernels/fa2.py:53, model.py:70-75).
@@ -50,7 +52,7 @@ enum mi_fa2_status {
   MI_FA2_ERR_LAUNCH = 4       /* the HIP runtime refused the launch */
 };
 
-enum mi_fa2_dtype { MI_FA2_BF16 = 0, MI_FA2_FP16 = 1 };
+enum mi_fa2_dtype { MI_FA2_BF16 = 0, MI_FA2_FP16 = 1, MI_FA2_FP32 = 2 };
 
 /* Library version string, e.g. "mi_fa2 0.1.0 gfx950". */
 MI_FA2_API const char* mi_fa2_version(void);
@@ -168,6 +170,26 @@ MI_FA2_API int mi_fa2_rope_kv_write(int32_t dtype, const void* qkv, int64_t qkv_
                                     int64_t q_row_stride, void* k_pool, void* v_pool,
                                     const int64_t* pool_strides, int32_t num_slots,
                                     mi_fa2_stream_t stream);
+
+/*
+ * Fused token sampler.  Replaces the reference's batched sampling (chat.py:103-107:
+ * probs = softmax(logits.float() / temperature); torch.multinomial(probs, 1)) applied to the
+ * last-position logits (model.py:204-207): draws one token per row of logits [batch, vocab]
+ * (row stride `row_stride` elements, dtype bf16, fp16 or fp32) into tokens [batch] int32.
+ *   temperature > 0: token = argmax_v(logit_v / temperature - ln E_v), E_v ~ Exp(1) -- the
+ *     exponential race torch.multinomial uses for one sample, so the distribution is
+ *     softmax(logits / temperature); E_v = -ln U_v with U_v from Philox4x32-10 keyed by `seed`,
+ *     counter (v / 4, row, offset): advance `offset` by one per call for fresh draws.
+ *   temperature <= 0: greedy argmax.
+ * Ties go to the lowest index; NaN logits never win; a row with no candidate (all -inf or NaN)
+ * gets -1 (torch.multinomial raises there).  batch <= 65535.  Needs the workspace that
+ * mi_fa2_sample_workspace_size() returns (0 when vocab <= 8192).  Asynchronous on `stream`.
+ */
+MI_FA2_API size_t mi_fa2_sample_workspace_size(int32_t batch, int32_t vocab);
+MI_FA2_API int mi_fa2_sample(int32_t dtype, const void* logits, int64_t row_stride, int32_t batch,
+                             int32_t vocab, float temperature, uint64_t seed, uint64_t offset,
+                             int32_t* tokens, void* workspace, size_t workspace_bytes,
+                             mi_fa2_stream_t stream);
 
 #ifdef __cplusplus
 }

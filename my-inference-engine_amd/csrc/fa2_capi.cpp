@@ -16,6 +16,8 @@ hipError_t launch_prefill(const FwdParams& p, int dtype, int mode, int max_seqle
                           hipStream_t stream);
 hipError_t launch_decode(const FwdParams& p, int dtype, int mode, hipStream_t stream);
 hipError_t launch_rope_kv(const RopeParams& p, int dtype, hipStream_t stream);
+hipError_t launch_sample(const SampleParams& p, int dtype, hipStream_t stream);
+int sample_chunks(int vocab);
 }  // namespace mi_fa2
 
 using mi_fa2::FwdParams;
@@ -419,4 +421,53 @@ int mi_fa2_rope_kv_write(int32_t dtype, const void* qkv, int64_t qkv_row_stride,
   p.Hq = heads_q;
   p.Hkv = heads_kv;
   return launched(mi_fa2::launch_rope_kv(p, dtype, reinterpret_cast<hipStream_t>(stream)));
+}
+
+size_t mi_fa2_sample_workspace_size(int32_t batch, int32_t vocab) {
+  if (batch <= 0 || vocab <= 0) return 0;
+  const int chunks = mi_fa2::sample_chunks(vocab);
+  return chunks > 1 ? (size_t)batch * chunks * (sizeof(float) + sizeof(int32_t)) : 0;
+}
+
+int mi_fa2_sample(int32_t dtype, const void* logits, int64_t row_stride, int32_t batch,
+                  int32_t vocab, float temperature, uint64_t seed, uint64_t offset, int32_t* tokens,
+                  void* workspace, size_t workspace_bytes, mi_fa2_stream_t stream) {
+  if (dtype != MI_FA2_BF16 && dtype != MI_FA2_FP16 && dtype != MI_FA2_FP32)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "dtype %d is not bf16 (0), fp16 (1) or fp32 (2)", dtype);
+  if (batch < 0 || vocab <= 0 || vocab > (1 << 30))
+    return fail(MI_FA2_ERR_INVALID, "bad sizes: batch=%d vocab=%d", batch, vocab);
+  if (batch > 65535)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "batch %d exceeds 65535 rows per call", batch);
+  if (temperature != temperature) return fail(MI_FA2_ERR_INVALID, "temperature is NaN");
+  if (batch == 0) return ok();
+  if (!logits) return fail(MI_FA2_ERR_INVALID, "logits is NULL");
+  if (!tokens) return fail(MI_FA2_ERR_INVALID, "tokens is NULL");
+  const uintptr_t elem = dtype == MI_FA2_FP32 ? 4 : 2;
+  if (reinterpret_cast<uintptr_t>(logits) % elem)
+    return fail(MI_FA2_ERR_INVALID, "logits is not aligned to its element size");
+  if (row_stride < vocab)
+    return fail(MI_FA2_ERR_INVALID, "row_stride %lld is shorter than a row of %d",
+                (long long)row_stride, vocab);
+  const size_t need = mi_fa2_sample_workspace_size(batch, vocab);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(MI_FA2_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
+                workspace ? workspace_bytes : (size_t)0);
+  mi_fa2::SampleParams p{};
+  p.logits = logits;
+  p.row_stride = row_stride;
+  p.tokens = tokens;
+  p.batch = batch;
+  p.vocab = vocab;
+  p.chunks = mi_fa2::sample_chunks(vocab);
+  p.greedy = temperature > 0.f ? 0 : 1;
+  p.inv_t = temperature > 0.f ? 1.f / temperature : 0.f;
+  p.seed_lo = (uint32_t)seed;
+  p.seed_hi = (uint32_t)(seed >> 32);
+  p.off_lo = (uint32_t)offset;
+  p.off_hi = (uint32_t)(offset >> 32);
+  if (need) {
+    p.part_s = static_cast<float*>(workspace);
+    p.part_i = reinterpret_cast<int32_t*>(p.part_s + (size_t)batch * p.chunks);
+  }
+  return launched(mi_fa2::launch_sample(p, dtype, reinterpret_cast<hipStream_t>(stream)));
 }

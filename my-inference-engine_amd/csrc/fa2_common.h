@@ -141,6 +141,18 @@ struct RopeParams {
   int32_t n_tokens, Hq, Hkv;
 };
 
+// Token sampler (sample.hip).
+struct SampleParams {
+  const void* logits;
+  int64_t row_stride;   // elements
+  int32_t* tokens;
+  float* part_s;        // [batch][chunks] best score of each chunk
+  int32_t* part_i;      // [batch][chunks] its index (-1: no candidate)
+  int batch, vocab, chunks, greedy;
+  float inv_t;
+  uint32_t seed_lo, seed_hi, off_lo, off_hi;
+};
+
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 // Raw buffer resource over [base, base + bytes): loads at offsets past `bytes` return zeros, which

@@ -12,7 +12,10 @@ globals and a daemon worker thread:
     the first reply token (chat.py:157-185); at most one admission per tick, so decoding jobs are
     not starved (chat.py:247-253);
   * every tick then runs ONE batched decode step for all active jobs (chat.py:257-308) and samples
-    every row with a single device sync (chat.py:103-107);
+    every row with a single device sync (chat.py:103-107); on the GPU the draw is one fused HIP
+    launch (kernels.sample.sample_tokens: the exponential race torch.multinomial uses, over a
+    Philox stream keyed by the engine's seed and advanced once per draw), on the CPU the
+    reference's softmax + multinomial;
   * a finished reply keeps its cache (the conversation continues), appends the separator and
     gives back reserved-but-unused blocks (chat.py:194-211).
 
@@ -30,6 +33,8 @@ from collections import deque
 from dataclasses import dataclass, field
 
 import torch
+
+from kernels.sample import sample_tokens
 
 
 @dataclass
@@ -66,7 +71,9 @@ class Engine:
         self.temperature = temperature
         self.sep_ids = list(sep_ids)   # appended after each reply, like "\n" (chat.py:200)
         self.device = next(model.parameters()).device
+        self.seed = seed
         self.gen = torch.Generator(device=self.device).manual_seed(seed)
+        self._draws = 0      # Philox offset of the fused sampler: one per sampling call
         self.queue = deque()
         self.active = []
         self.deferred = []
@@ -263,6 +270,12 @@ class Engine:
 
     def _sample(self, logits):
         """One id per row of [B, vocab] logits, one device sync for all rows (chat.py:103-107)."""
+        if logits.is_cuda:
+            toks = sample_tokens(logits, self.temperature, self.seed, self._draws).tolist()
+            self._draws += 1
+            if min(toks) < 0:
+                raise RuntimeError("a row of logits has no finite entry to sample from")
+            return toks
         probs = torch.softmax(logits.float() / self.temperature, dim=-1)
         return torch.multinomial(probs, 1, generator=self.gen).squeeze(1).tolist()
 

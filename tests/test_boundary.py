@@ -22,7 +22,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     names = declared_symbols()
-    assert len(names) == 9
+    assert len(names) == 11
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_lib.SIGNATURES)
@@ -52,6 +52,9 @@ def test_workspace_sizes():
     assert n == 64 * 12 * (8192 // 128) * 130 * 4 + 64 * 2 * 4
     # a single short row fits in one split: no workspace
     assert lib.mi_fa2_fwd_workspace_size(1, 12, 2, 1, 100, 128) == 0
+    # the sampler: one (score, index) partial per 8192-entry chunk of each row, none for one chunk
+    assert lib.mi_fa2_sample_workspace_size(16, 151936) == 16 * 19 * 8
+    assert lib.mi_fa2_sample_workspace_size(4, 8192) == 0
 
 
 def _fwd(lib, **over):
@@ -109,3 +112,33 @@ def test_stride_helper_zeroes_size_one_dims():
     assert s == [640, 0, 128, 1]
     assert fa2._dims_ok(torch.empty(2, 12, 7, 128))
     assert not fa2._dims_ok(torch.empty(2, 12, 7, 128).transpose(-1, -2))
+
+
+def _sample(lib, **over):
+    a = dict(dtype=0, logits=16, row_stride=1000, batch=2, vocab=1000, temperature=1.0,
+             tokens=16, ws=None, ws_bytes=0)
+    a.update(over)
+    return lib.mi_fa2_sample(a["dtype"], a["logits"], a["row_stride"], a["batch"], a["vocab"],
+                             a["temperature"], 0, 0, a["tokens"], a["ws"], a["ws_bytes"], None)
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(dtype=5), 2, "dtype"),
+    (dict(logits=None), 1, "logits is NULL"),
+    (dict(tokens=None), 1, "tokens is NULL"),
+    (dict(dtype=2, logits=18), 1, "aligned"),
+    (dict(row_stride=999), 1, "row_stride"),
+    (dict(temperature=float("nan")), 1, "NaN"),
+    (dict(vocab=0), 1, "bad sizes"),
+    (dict(batch=70000), 2, "65535"),
+    (dict(vocab=20000, row_stride=20000), 3, "workspace"),
+])
+def test_sampler_rejects_bad_arguments_before_any_launch(over, status, msg):
+    lib = _lib.load()
+    assert _sample(lib, **over) == status
+    assert msg in lib.mi_fa2_last_error().decode()
+
+
+def test_sampler_zero_rows_is_a_no_op():
+    lib = _lib.load()
+    assert _sample(lib, batch=0, logits=None, tokens=None) == 0
