@@ -191,6 +191,31 @@ MI_FA2_API int mi_fa2_sample(int32_t dtype, const void* logits, int64_t row_stri
                              int32_t* tokens, void* workspace, size_t workspace_bytes,
                              mi_fa2_stream_t stream);
 
+/*
+ * Per-step paged-cache metadata from device-resident block tables.  Replaces the host side of
+ * KVCache.prepare (kv_cache.py:74-101: a Python loop over every new token for slot_mapping, a
+ * dense gather index, two host-to-device copies per step, consumed at model.py:168-175):
+ *   tables [max_seqs, table_stride] int32: each sequence slot's block ids, kept on the device and
+ *     written only when blocks are allocated; seq_lens [max_seqs] int32: tokens each slot holds,
+ *     ADVANCED IN PLACE by this call (row b's slot grows by its token count);
+ *   row_slots [batch] int32: the slot of each row (< 0: a padding row: no keys, slot -1 for its
+ *     tokens, no advance); distinct rows must name distinct slots;
+ *   cu [batch + 1] int32: row b's new tokens are [cu[b], cu[b+1]) of the packed batch, or NULL:
+ *     every row has tokens_per_row tokens, row b's at b * tokens_per_row;
+ * and writes starts [batch] (length before the step), kv_lens [batch] (= starts + count),
+ * block_table [batch, width] (the first ceil(kv_len / block_size) entries of the slot's table,
+ * then 0), slots [tokens] (cache slot of every new token, kv_cache.py:15-16), and optionally
+ * positions [tokens] and last_idx [batch] (packed index of each row's last token).  A row whose
+ * keys would not fit its table row is treated as padding.  All pointers are device pointers; one
+ * launch, asynchronous on `stream`, safe to capture in a graph.
+ */
+MI_FA2_API int mi_fa2_step_metadata(const int32_t* row_slots, const int32_t* cu,
+                                    int32_t tokens_per_row, int32_t batch, int32_t* seq_lens,
+                                    int32_t max_seqs, const int32_t* tables, int64_t table_stride,
+                                    int32_t block_size, int32_t width, int32_t* starts,
+                                    int32_t* kv_lens, int32_t* block_table, int32_t* slots,
+                                    int32_t* positions, int32_t* last_idx, mi_fa2_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,7 @@ hipError_t launch_decode(const FwdParams& p, int dtype, int mode, hipStream_t st
 hipError_t launch_rope_kv(const RopeParams& p, int dtype, hipStream_t stream);
 hipError_t launch_sample(const SampleParams& p, int dtype, hipStream_t stream);
 int sample_chunks(int vocab);
+hipError_t launch_step_meta(const StepMetaParams& p, hipStream_t stream);
 }  // namespace mi_fa2
 
 using mi_fa2::FwdParams;
@@ -470,4 +471,41 @@ int mi_fa2_sample(int32_t dtype, const void* logits, int64_t row_stride, int32_t
     p.part_i = reinterpret_cast<int32_t*>(p.part_s + (size_t)batch * p.chunks);
   }
   return launched(mi_fa2::launch_sample(p, dtype, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int mi_fa2_step_metadata(const int32_t* row_slots, const int32_t* cu, int32_t tokens_per_row,
+                         int32_t batch, int32_t* seq_lens, int32_t max_seqs, const int32_t* tables,
+                         int64_t table_stride, int32_t block_size, int32_t width, int32_t* starts,
+                         int32_t* kv_lens, int32_t* block_table, int32_t* slots,
+                         int32_t* positions, int32_t* last_idx, mi_fa2_stream_t stream) {
+  if (batch < 0 || max_seqs <= 0 || table_stride <= 0 || block_size <= 0 || width <= 0 ||
+      (!cu && tokens_per_row < 0))
+    return fail(MI_FA2_ERR_INVALID,
+                "bad sizes: batch=%d max_seqs=%d table_stride=%lld block_size=%d width=%d "
+                "tokens_per_row=%d", batch, max_seqs, (long long)table_stride, block_size, width,
+                tokens_per_row);
+  if (batch == 0) return ok();
+  const void* ptrs[] = {row_slots, seq_lens, tables, starts, kv_lens, block_table, slots};
+  const char* names[] = {"row_slots", "seq_lens", "tables", "starts", "kv_lens", "block_table",
+                         "slots"};
+  for (int i = 0; i < 7; ++i)
+    if (!ptrs[i]) return fail(MI_FA2_ERR_INVALID, "%s is NULL", names[i]);
+  mi_fa2::StepMetaParams p{};
+  p.row_slots = row_slots;
+  p.cu = cu;
+  p.T = tokens_per_row;
+  p.B = batch;
+  p.W = width;
+  p.block_size = block_size;
+  p.max_seqs = max_seqs;
+  p.seq_lens = seq_lens;
+  p.tables = tables;
+  p.table_stride = table_stride;
+  p.starts = starts;
+  p.kv_lens = kv_lens;
+  p.block_table = block_table;
+  p.slots = slots;
+  p.positions = positions;
+  p.last_idx = last_idx;
+  return launched(mi_fa2::launch_step_meta(p, reinterpret_cast<hipStream_t>(stream)));
 }

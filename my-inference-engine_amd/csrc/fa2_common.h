@@ -153,6 +153,22 @@ struct SampleParams {
   uint32_t seed_lo, seed_hi, off_lo, off_hi;
 };
 
+// Per-step paged-cache metadata (step_meta.hip).
+struct StepMetaParams {
+  const int32_t* row_slots;  // [B] sequence slot of each row, < 0: padding row
+  const int32_t* cu;         // [B + 1] packed token offsets, or NULL: row b holds tokens b*T ..
+  int32_t T, B, W, block_size, max_seqs;
+  int32_t* seq_lens;         // [max_seqs] tokens held per slot, advanced in place
+  const int32_t* tables;     // [max_seqs][table_stride] block ids per slot
+  int64_t table_stride;
+  int32_t* starts;           // [B]
+  int32_t* kv_lens;          // [B]
+  int32_t* block_table;      // [B][W]
+  int32_t* slots;            // [N]
+  int32_t* positions;        // [N] or NULL
+  int32_t* last_idx;         // [B] or NULL
+};
+
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 // Raw buffer resource over [base, base + bytes): loads at offsets past `bytes` return zeros, which

@@ -19,6 +19,14 @@ numpy and ONE pinned host-to-device copy, exactly what the paged kernel reads:
 and no per-layer gather happens on the GPU path.  read() (the dense gather) is kept for the CPU
 fallback and for reference-compatible callers.
 
+On the GPU the tables themselves are device-resident (device_tables, the default there): every
+sequence holds a slot with a row of `dev_tables` [max_seqs, num_blocks] int32 and a length in
+`dev_lens` [max_seqs] int32.  A table row is written only when blocks are allocated
+(ensure_capacity: one small copy per allocation), and a step sends only its rows' slots: one HIP
+launch (kernels.meta.step_metadata, csrc/step_meta.hip) derives starts, kv_lens, the batch block
+table, every new token's slot (and positions / last indices for mixed steps) and advances the
+device lengths in place.  The host keeps the same tables and lengths for scheduling decisions.
+
 prepare_packed() builds the metadata of a mixed step, where each row appends its own number of
 tokens (one for a decoding chat, a whole prompt for a newly admitted one) and the rows' tokens are
 packed back to back: prefix offsets cu_q, every token's position and slot, and each row's last
@@ -104,7 +112,8 @@ class PackedMeta:
 
 
 class KVCache:
-    def __init__(self, num_blocks, block_size, device, dtype, num_layers, num_kv_heads, head_dim):
+    def __init__(self, num_blocks, block_size, device, dtype, num_layers, num_kv_heads, head_dim,
+                 *, device_tables=None, max_seqs=256):
         self.buf = torch.zeros(num_layers, 2, num_blocks * block_size, num_kv_heads, head_dim,
                                device=device, dtype=dtype)
         self.num_blocks = num_blocks
@@ -114,6 +123,14 @@ class KVCache:
         self._block_tables = {}   # seq id -> list of block ids, in logical order
         self._lengths = {}        # seq id -> tokens written so far
         self._next_seq = 0
+        self.device_tables = self.device.type == "cuda" if device_tables is None else device_tables
+        if self.device_tables:
+            assert self.device.type == "cuda", "device-resident tables need a GPU cache"
+            self.max_seqs = max_seqs
+            self.dev_tables = torch.zeros(max_seqs, num_blocks, dtype=torch.int32, device=device)
+            self.dev_lens = torch.zeros(max_seqs, dtype=torch.int32, device=device)
+            self._free_slots = list(range(max_seqs - 1, -1, -1))
+            self.slot = {}        # seq id -> row of dev_tables / dev_lens
 
     # -- bookkeeping (kv_cache.py:31-72) -------------------------------------------------------
     def free_block_count(self):
@@ -124,15 +141,24 @@ class KVCache:
         return max(0, math.ceil(total_len / self.block_size) - held)
 
     def alloc(self):
+        if self.device_tables:
+            if not self._free_slots:
+                raise RuntimeError(f"all {self.max_seqs} device table slots are in use")
+            slot = self._free_slots.pop()
         seq = self._next_seq
         self._next_seq += 1
         self._block_tables[seq] = []
         self._lengths[seq] = 0
+        if self.device_tables:
+            self.slot[seq] = slot
+            self.dev_lens[slot:slot + 1].zero_()
         return seq
 
     def free(self, seq):
         self._free_blocks.extend(self._block_tables.pop(seq))
         del self._lengths[seq]
+        if self.device_tables:
+            self._free_slots.append(self.slot.pop(seq))
 
     def length(self, seq):
         return self._lengths[seq]
@@ -143,8 +169,12 @@ class KVCache:
             raise RuntimeError(f"KV cache exhausted: seq {seq} needs {need} more blocks, "
                                f"only {len(self._free_blocks)} free")
         table = self._block_tables[seq]
+        old = len(table)
         for _ in range(need):
             table.append(self._free_blocks.pop())
+        if self.device_tables and need:
+            new = torch.tensor(table[old:], dtype=torch.int32)
+            self.dev_tables[self.slot[seq], old:old + need].copy_(new)
 
     def trim(self, seq):
         table = self._block_tables[seq]
@@ -191,6 +221,8 @@ class KVCache:
         return host, starts, W
 
     def prepare(self, seqs, T):
+        if self.device_tables:
+            return self._prepare_device(seqs, [T] * len(seqs), packed=False)
         B = len(seqs)
         host, starts, W = self.pack_step(seqs, T)
         tables = [self._block_tables[s] for s in seqs]
@@ -211,6 +243,8 @@ class KVCache:
         """Grow the rows' tables for counts[b] new tokens each and build a PackedMeta with one
         pinned host-to-device copy of [cu_q | kv_lens | positions | slots | last_idx | tables]."""
         assert len(seqs) == len(counts) and len(seqs) > 0 and min(counts) >= 1
+        if self.device_tables:
+            return self._prepare_device(seqs, counts, packed=True)
         bs = self.block_size
         starts = [self._lengths[s] for s in seqs]
         for s, start, c in zip(seqs, starts, counts):
@@ -249,6 +283,42 @@ class KVCache:
             slot_mapping32=dev[o + N:o + 2 * N], last_idx=dev[o + 2 * N:o + 2 * N + B],
             block_table=dev[o + 2 * N + B:].view(B, W), tables=[list(t) for t in tables])
 
+    def _prepare_device(self, seqs, counts, packed):
+        """The device-table path of prepare / prepare_packed: one pinned copy of the rows' slots
+        (and packed offsets), one metadata launch; tables and lengths never leave the device."""
+        from kernels.meta import step_metadata
+        assert len(set(seqs)) == len(seqs), "a sequence may appear once per step"
+        bs = self.block_size
+        starts = [self._lengths[s] for s in seqs]
+        for s, start, c in zip(seqs, starts, counts):
+            self.ensure_capacity(s, start + c)
+        B, N = len(seqs), sum(counts)
+        W = max(1, math.ceil(max(st + c for st, c in zip(starts, counts)) / bs))
+        host = np.empty(B + (B + 1 if packed else 0), dtype=np.int32)
+        host[:B] = [self.slot[s] for s in seqs]
+        if packed:
+            host[B] = 0
+            np.cumsum(np.asarray(counts, dtype=np.int32), out=host[B + 1:])
+        small = torch.from_numpy(host).pin_memory().to(self.device, non_blocking=True)
+        row_slots, cu = small[:B], (small[B:] if packed else None)
+        out = torch.empty(3 * B + B * W + 2 * N, dtype=torch.int32, device=self.device)
+        o_starts, o_kv, o_last = out[:B], out[B:2 * B], out[2 * B:3 * B]
+        o_bt = out[3 * B:3 * B + B * W].view(B, W)
+        o_slots, o_pos = out[3 * B + B * W:3 * B + B * W + N], out[3 * B + B * W + N:]
+        step_metadata(self, row_slots, cu, counts[0], o_starts, o_kv, o_bt, o_slots,
+                      o_pos if packed else None, o_last if packed else None)
+        tables = [list(self._block_tables[s]) for s in seqs]
+        if not packed:
+            return StepMeta(starts=starts, T=counts[0], block_size=bs, starts_dev=o_starts,
+                            kv_lens=o_kv, slot_mapping=None, block_table=o_bt,
+                            slot_mapping32=o_slots, tables=tables)
+        n_single = 0
+        while n_single < B and counts[n_single] == 1:
+            n_single += 1
+        return PackedMeta(starts=starts, counts=list(counts), block_size=bs, n_single=n_single,
+                          cu_q=cu, kv_lens=o_kv, positions=o_pos, slot_mapping32=o_slots,
+                          last_idx=o_last, block_table=o_bt, tables=tables)
+
     # -- data movement --------------------------------------------------------------------------
     def k_pool(self, layer):
         return self.buf[layer, 0]
@@ -259,8 +329,9 @@ class KVCache:
     def write(self, layer, meta, k, v):
         """Scatter this step's k/v [B, Hkv, T, d] into their slots (kv_cache.py:108-115)."""
         B, H, T, D = k.shape
-        self.buf[layer, 0].index_copy_(0, meta.slot_mapping, k.transpose(1, 2).reshape(B * T, H, D))
-        self.buf[layer, 1].index_copy_(0, meta.slot_mapping, v.transpose(1, 2).reshape(B * T, H, D))
+        sm = meta.slot_mapping if meta.slot_mapping is not None else meta.slot_mapping32.long()
+        self.buf[layer, 0].index_copy_(0, sm, k.transpose(1, 2).reshape(B * T, H, D))
+        self.buf[layer, 1].index_copy_(0, sm, v.transpose(1, 2).reshape(B * T, H, D))
 
     def read_row(self, layer, table, n):
         """Dense [Hkv, n, d] copies of the first n keys/values of the sequence whose block list is
