@@ -216,6 +216,30 @@ MI_FA2_API int mi_fa2_step_metadata(const int32_t* row_slots, const int32_t* cu,
                                     int32_t* kv_lens, int32_t* block_table, int32_t* slots,
                                     int32_t* positions, int32_t* last_idx, mi_fa2_stream_t stream);
 
+/*
+ * Fused residual add + RMSNorm.  Replaces, on the GPU path, the reference's residual add
+ * (model.py:128-138: x = x + attn / x = x + mlp) followed by the next RMSNorm (model.py:49-55: eight
+ * torch ops), keeping their rounding points:
+ *   r = round(x + y)                       (r = x when y is NULL), written to residual_out;
+ *   out = round(weight * round(float(r) * rsqrt(mean(float(r)^2) + eps))).
+ * x, y, residual_out, out [rows, hidden] with row strides (elements, multiples of 8, 16-byte
+ * aligned bases); weight [hidden].  hidden: a multiple of 8, at most 8192.  residual_out may be x
+ * itself (in place).  Asynchronous on `stream`.
+ */
+MI_FA2_API int mi_fa2_add_rmsnorm(int32_t dtype, const void* x, int64_t x_stride, const void* y,
+                                  int64_t y_stride, const void* weight, void* residual_out,
+                                  int64_t residual_stride, void* out, int64_t out_stride,
+                                  int32_t rows, int32_t hidden, float eps, mi_fa2_stream_t stream);
+
+/*
+ * SwiGLU activation.  Replaces F.silu(gate) * up (model.py:112-120) on the fused gate|up
+ * projection: gate_up [rows, 2 * inter] (gate columns first) -> out [rows, inter],
+ * out = round(round(g / (1 + exp(-g))) * u).  inter: a multiple of 8.  Asynchronous on `stream`.
+ */
+MI_FA2_API int mi_fa2_silu_mul(int32_t dtype, const void* gate_up, int64_t gate_up_stride,
+                               void* out, int64_t out_stride, int32_t rows, int32_t inter,
+                               mi_fa2_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,6 +19,8 @@ hipError_t launch_rope_kv(const RopeParams& p, int dtype, hipStream_t stream);
 hipError_t launch_sample(const SampleParams& p, int dtype, hipStream_t stream);
 int sample_chunks(int vocab);
 hipError_t launch_step_meta(const StepMetaParams& p, hipStream_t stream);
+hipError_t launch_add_rmsnorm(const ModelOpParams& p, int dtype, hipStream_t stream);
+hipError_t launch_silu_mul(const ModelOpParams& p, int dtype, hipStream_t stream);
 }  // namespace mi_fa2
 
 using mi_fa2::FwdParams;
@@ -508,4 +510,68 @@ int mi_fa2_step_metadata(const int32_t* row_slots, const int32_t* cu, int32_t to
   p.positions = positions;
   p.last_idx = last_idx;
   return launched(mi_fa2::launch_step_meta(p, reinterpret_cast<hipStream_t>(stream)));
+}
+
+namespace {
+int check_rows(const char* name, const void* ptr, int64_t stride, int64_t min_stride) {
+  if (!ptr) return fail(MI_FA2_ERR_INVALID, "%s is NULL", name);
+  if (!aligned16(ptr)) return fail(MI_FA2_ERR_INVALID, "%s is not 16-byte aligned", name);
+  if (stride < min_stride || stride % 8)
+    return fail(MI_FA2_ERR_INVALID, "%s row stride %lld: a multiple of 8 of at least %lld needed",
+                name, (long long)stride, (long long)min_stride);
+  return MI_FA2_OK;
+}
+}  // namespace
+
+int mi_fa2_add_rmsnorm(int32_t dtype, const void* x, int64_t x_stride, const void* y,
+                       int64_t y_stride, const void* weight, void* residual_out,
+                       int64_t residual_stride, void* out, int64_t out_stride, int32_t rows,
+                       int32_t hidden, float eps, mi_fa2_stream_t stream) {
+  if (dtype != MI_FA2_BF16 && dtype != MI_FA2_FP16)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "dtype %d is not bf16 (0) or fp16 (1)", dtype);
+  if (rows < 0 || hidden <= 0 || hidden % 8 || hidden > 8192)
+    return fail(MI_FA2_ERR_INVALID, "bad sizes: rows=%d hidden=%d (hidden: a multiple of 8, <= 8192)",
+                rows, hidden);
+  if (rows == 0) return ok();
+  if (int rc = check_rows("x", x, x_stride, hidden)) return rc;
+  if (y)
+    if (int rc = check_rows("y", y, y_stride, hidden)) return rc;
+  if (residual_out)
+    if (int rc = check_rows("residual_out", residual_out, residual_stride, hidden)) return rc;
+  if (int rc = check_rows("out", out, out_stride, hidden)) return rc;
+  if (!weight || !aligned16(weight))
+    return fail(MI_FA2_ERR_INVALID, "weight is NULL or not 16-byte aligned");
+  mi_fa2::ModelOpParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.x_st = x_stride;
+  p.y = static_cast<const uint16_t*>(y);
+  p.y_st = y_stride;
+  p.weight = static_cast<const uint16_t*>(weight);
+  p.r_out = y ? static_cast<uint16_t*>(residual_out) : nullptr;
+  p.r_st = residual_stride;
+  p.out = static_cast<uint16_t*>(out);
+  p.out_st = out_stride;
+  p.rows = rows;
+  p.hidden = hidden;
+  p.eps = eps;
+  return launched(mi_fa2::launch_add_rmsnorm(p, dtype, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int mi_fa2_silu_mul(int32_t dtype, const void* gate_up, int64_t gate_up_stride, void* out,
+                    int64_t out_stride, int32_t rows, int32_t inter, mi_fa2_stream_t stream) {
+  if (dtype != MI_FA2_BF16 && dtype != MI_FA2_FP16)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "dtype %d is not bf16 (0) or fp16 (1)", dtype);
+  if (rows < 0 || inter <= 0 || inter % 8)
+    return fail(MI_FA2_ERR_INVALID, "bad sizes: rows=%d inter=%d (a multiple of 8)", rows, inter);
+  if (rows == 0) return ok();
+  if (int rc = check_rows("gate_up", gate_up, gate_up_stride, 2 * (int64_t)inter)) return rc;
+  if (int rc = check_rows("out", out, out_stride, inter)) return rc;
+  mi_fa2::ModelOpParams p{};
+  p.x = static_cast<const uint16_t*>(gate_up);
+  p.x_st = gate_up_stride;
+  p.out = static_cast<uint16_t*>(out);
+  p.out_st = out_stride;
+  p.rows = rows;
+  p.hidden = inter;
+  return launched(mi_fa2::launch_silu_mul(p, dtype, reinterpret_cast<hipStream_t>(stream)));
 }

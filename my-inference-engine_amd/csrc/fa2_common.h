@@ -153,6 +153,21 @@ struct SampleParams {
   uint32_t seed_lo, seed_hi, off_lo, off_hi;
 };
 
+// Fused residual-add + RMSNorm and SiLU x up (model_ops.hip).
+struct ModelOpParams {
+  const uint16_t* x;    // [rows][x_st]: rows to normalise (or gate|up rows for silu_mul)
+  int64_t x_st;
+  const uint16_t* y;    // [rows][y_st]: added to x first, or NULL
+  int64_t y_st;
+  const uint16_t* weight;  // [hidden]
+  uint16_t* r_out;      // [rows][r_st]: x + y, or NULL
+  int64_t r_st;
+  uint16_t* out;        // [rows][out_st]
+  int64_t out_st;
+  int32_t rows, hidden;
+  float eps;
+};
+
 // Per-step paged-cache metadata (step_meta.hip).
 struct StepMetaParams {
   const int32_t* row_slots;  // [B] sequence slot of each row, < 0: padding row

@@ -11,6 +11,9 @@ logits (model.py:204-207) -- with two deliberate differences on the GPU path:
   * The q/k/v and gate/up projections are single fused GEMMs (one launch instead of three/two).
   * RoPE and the cache write are one HIP launch (kernels.rope.rope_kv_write) instead of the
     elementwise RoPE ops and two index_copy_ (model.py:92,96), with bitwise the same results.
+  * Each residual add and the RMSNorm after it are one HIP launch (kernels.model_ops.add_rmsnorm)
+    and SiLU x up is one more (kernels.model_ops.silu_mul), instead of about twenty small torch
+    launches per layer, with the same rounding points.
 
 forward_mixed() runs one step over rows that append different numbers of tokens -- decoding chats
 (one token each) and newly admitted prompts -- packed back to back: every projection, norm and MLP
@@ -30,6 +33,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from kernels.fa2 import fa2_paged, fa2_paged_varlen
+from kernels.model_ops import add_rmsnorm, silu_mul
 from kernels.rope import rope_kv_write
 
 
@@ -58,6 +62,9 @@ class RMSNorm(nn.Module):
         self.eps = eps
 
     def forward(self, x):
+        if x.is_cuda:
+            shape = x.shape
+            return add_rmsnorm(x.reshape(-1, shape[-1]), self.weight, self.eps)[1].view(shape)
         dtype = x.dtype
         xf = x.float()
         xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
@@ -163,7 +170,11 @@ class MLP(nn.Module):
         self.down_proj = nn.Linear(cfg.intermediate_size, cfg.hidden_size, bias=False)
 
     def forward(self, x):
-        gate, up = self.gate_up_proj(x).split(self.inter, dim=-1)
+        gu = self.gate_up_proj(x)
+        if x.is_cuda:
+            act = silu_mul(gu.view(-1, 2 * self.inter)).view(*gu.shape[:-1], self.inter)
+            return self.down_proj(act)
+        gate, up = gu.split(self.inter, dim=-1)
         return self.down_proj(F.silu(gate) * up)
 
 
@@ -224,10 +235,32 @@ class Qwen2ForCausalLM(nn.Module):
         x = self.embed_tokens(input_ids)
         position_ids = meta.starts_dev[:, None] + torch.arange(T, device=x.device)[None, :]
         cos, sin = self.rope_cos_sin(position_ids, x.dtype)
-        for layer_idx, layer in enumerate(self.layers):
-            x = layer(x, cos, sin, cache, layer_idx, meta)
+        x = self.run_layers(x, cos, sin, cache, meta)
         x = self.norm(x[:, -1:])
         return x @ self.embed_tokens.weight.T
+
+    def run_layers(self, x, cos, sin, cache, meta):
+        """The decoder layers over x [B, T, hidden].  On the GPU each residual add is fused with the
+        RMSNorm that follows it (the first layer's input norm has no add; the last layer's MLP
+        output is added alone), which is the same arithmetic as Block.forward layer by layer."""
+        if not x.is_cuda:
+            for layer_idx, layer in enumerate(self.layers):
+                x = layer(x, cos, sin, cache, layer_idx, meta)
+            return x
+        shape, H, eps = x.shape, x.shape[-1], self.cfg.rms_norm_eps
+        res = x.reshape(-1, H)
+        _, h = add_rmsnorm(res, self.layers[0].input_layernorm.weight, eps)
+        for i, layer in enumerate(self.layers):
+            a = layer.self_attn(h.view(shape), cos, sin, cache, i, meta).reshape(-1, H)
+            res, h = add_rmsnorm(res, layer.post_attention_layernorm.weight, eps, y=a,
+                                 residual_out=res)
+            m = layer.mlp(h.view(shape)).reshape(-1, H)
+            if i + 1 < len(self.layers):
+                res, h = add_rmsnorm(res, self.layers[i + 1].input_layernorm.weight, eps, y=m,
+                                     residual_out=res)
+            else:
+                res = res + m
+        return res.view(shape)
 
     def forward_mixed(self, rows, cache, seqs):
         """One packed step: rows[b] (a list of token ids, at least one) is appended to cache
@@ -246,7 +279,6 @@ class Qwen2ForCausalLM(nn.Module):
         rows' new tokens back to back; returns the rows' last-token logits [B, vocab]."""
         x = self.embed_tokens(token_ids)[None]                      # [1, N, hidden]
         cos, sin = self.rope_cos_sin(meta.positions[None], x.dtype)
-        for layer_idx, layer in enumerate(self.layers):
-            x = layer(x, cos, sin, cache, layer_idx, meta)
+        x = self.run_layers(x, cos, sin, cache, meta)
         x = self.norm(x[0, meta.last_idx.long()])
         return x @ self.embed_tokens.weight.T

@@ -22,7 +22,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     names = declared_symbols()
-    assert len(names) == 12
+    assert len(names) == 14
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_lib.SIGNATURES)
@@ -142,3 +142,20 @@ def test_sampler_rejects_bad_arguments_before_any_launch(over, status, msg):
 def test_sampler_zero_rows_is_a_no_op():
     lib = _lib.load()
     assert _sample(lib, batch=0, logits=None, tokens=None) == 0
+
+
+def test_model_ops_reject_bad_arguments():
+    lib = _lib.load()
+    assert lib.mi_fa2_add_rmsnorm(0, 16, 1536, None, 0, 16, None, 0, 16, 1536, 2, 1540, 1e-6,
+                                  None) == 1
+    assert "hidden" in lib.mi_fa2_last_error().decode()
+    assert lib.mi_fa2_add_rmsnorm(0, 16, 8200, None, 0, 16, None, 0, 16, 8200, 2, 8200, 1e-6,
+                                  None) == 1
+    assert lib.mi_fa2_add_rmsnorm(0, 24, 1536, None, 0, 16, None, 0, 16, 1536, 2, 1536, 1e-6,
+                                  None) == 1
+    assert "aligned" in lib.mi_fa2_last_error().decode()
+    assert lib.mi_fa2_add_rmsnorm(3, 16, 1536, None, 0, 16, None, 0, 16, 1536, 2, 1536, 1e-6,
+                                  None) == 2
+    assert lib.mi_fa2_silu_mul(0, 16, 100, 16, 64, 2, 64, None) == 1
+    assert "gate_up" in lib.mi_fa2_last_error().decode()
+    assert lib.mi_fa2_silu_mul(0, 16, 128, 16, 64, 0, 64, None) == 0     # no rows: no-op
