@@ -14,6 +14,10 @@ logits (model.py:204-207) -- with two deliberate differences on the GPU path:
   * Each residual add and the RMSNorm after it are one HIP launch (kernels.model_ops.add_rmsnorm)
     and SiLU x up is one more (kernels.model_ops.silu_mul), instead of about twenty small torch
     launches per layer, with the same rounding points.
+  * The gate/up GEMM and the tied lm_head multiply by a cached transposed copy of their weight
+    ([in, out] row-major): at decode sizes hipBLASLt picks much faster kernels for that layout of
+    these two shapes (the other projections are faster as they are).  The parameters keep the
+    reference's layout; the copy is rebuilt if a weight changes.
 
 forward_mixed() runs one step over rows that append different numbers of tokens -- decoding chats
 (one token each) and newly admitted prompts -- packed back to back: every projection, norm and MLP
@@ -78,6 +82,15 @@ def rotate_half(x):
 
 def apply_rope(q, k, cos, sin):
     return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
+
+
+def transposed(weight):
+    """weight.t().contiguous(), cached on the parameter and rebuilt when it is modified."""
+    cached = getattr(weight, "_mi_transposed", None)
+    if cached is None or cached[0] != weight._version:
+        cached = (weight._version, weight.detach().t().contiguous())
+        weight._mi_transposed = cached
+    return cached[1]
 
 
 def repeat_kv(x, n_rep):
@@ -170,10 +183,11 @@ class MLP(nn.Module):
         self.down_proj = nn.Linear(cfg.intermediate_size, cfg.hidden_size, bias=False)
 
     def forward(self, x):
-        gu = self.gate_up_proj(x)
         if x.is_cuda:
-            act = silu_mul(gu.view(-1, 2 * self.inter)).view(*gu.shape[:-1], self.inter)
+            gu = x.reshape(-1, x.shape[-1]) @ transposed(self.gate_up_proj.weight)
+            act = silu_mul(gu).view(*x.shape[:-1], self.inter)
             return self.down_proj(act)
+        gu = self.gate_up_proj(x)
         gate, up = gu.split(self.inter, dim=-1)
         return self.down_proj(F.silu(gate) * up)
 
@@ -237,6 +251,12 @@ class Qwen2ForCausalLM(nn.Module):
         cos, sin = self.rope_cos_sin(position_ids, x.dtype)
         x = self.run_layers(x, cos, sin, cache, meta)
         x = self.norm(x[:, -1:])
+        return self.lm_head(x)
+
+    def lm_head(self, x):
+        """Tied-embedding logits (model.py:204-207)."""
+        if x.is_cuda:
+            return x @ transposed(self.embed_tokens.weight)
         return x @ self.embed_tokens.weight.T
 
     def run_layers(self, x, cos, sin, cache, meta):
@@ -281,4 +301,4 @@ class Qwen2ForCausalLM(nn.Module):
         cos, sin = self.rope_cos_sin(meta.positions[None], x.dtype)
         x = self.run_layers(x, cos, sin, cache, meta)
         x = self.norm(x[0, meta.last_idx.long()])
-        return x @ self.embed_tokens.weight.T
+        return self.lm_head(x)
