@@ -216,7 +216,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   // block, the tile's 64 rows need not) and skips tiles outside [0, kv_hi).
   const uint32_t lds_base = lds_addr_of(smem);
   auto dma_one = [&](const uint16_t* base, int64_t off, int64_t st, int ts, int lds_off, int voff,
-                     int h) {
+                     int h, int blk_pre) {
     const int i = wave + 8 * h;
     const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_base + lds_off + 1024 * i);
     if constexpr (is_paged(MODE)) {
@@ -226,7 +226,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
       const uint16_t* ptr = base;
       if (n > 0) {
         const int bs_shift = __builtin_ctz(p.block_size);
-        const int blk = p.block_table[(int64_t)b * p.bt_stride + (r0 >> bs_shift)];
+        const int blk = blk_pre;  // table entry of block r0 >> bs_shift, fetched a step ahead
         if ((unsigned)blk < (unsigned)p.num_blocks)
           ptr = base + off + (((int64_t)blk << bs_shift) + (r0 & (p.block_size - 1))) * st;
         else
@@ -254,22 +254,43 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   auto v0_start = [&](int j) { return j * kPfStep; };
   auto v1_start = [&](int j) { return (j - 1) * kPfStep + kPfBc; };
 
+  // Paged modes: the block-table entries of this wave's 8 load instructions of stage j, one per
+  // lane (lane q: K instruction q; lane 4 + q: V instruction q; -1 where nothing is loaded).  A
+  // table read is a vector load, and a wait for it would also wait for every LDS load in flight
+  // (the compiler cannot count those), so each stage's entries are fetched during the step before
+  // the one that issues its loads and arrive with that step's own loads.
+  auto tbl_fetch = [&](int j) -> int {
+    if constexpr (is_paged(MODE)) {
+      const int t = (lane >> 1) & 3, h = lane & 1;
+      const int ts = t == 0 ? k0_start(j) : t == 1 ? k1_start(j) : t == 2 ? v0_start(j) : v1_start(j);
+      const int r0 = ts + 4 * (wave + 8 * h);
+      if (lane < 8 && ts >= 0 && ts < kv_hi && r0 < kv_hi)
+        return p.block_table[(int64_t)b * p.bt_stride + (r0 >> __builtin_ctz(p.block_size))];
+      return -1;
+    } else {
+      return 0;
+    }
+  };
+
   // The 8 load instructions of a wave for stage j (which goes to LDS slot j & 1): 4 for K tiles,
   // 4 for V tiles, q = 2*tile + h.  Inside the key loop they are issued one at a time between the
-  // MFMAs of the score and PV phases rather than as a burst.
-  auto dma_k = [&](int j, int q) {
+  // MFMAs of the score and PV phases rather than as a burst.  `tbl` holds stage j's table entries.
+  auto dma_k = [&](int j, int q, int tbl) {
     const int o = (j & 1) * kStageBytes + (q >> 1) * kTileBytes;  // j & 1 folds when j's parity is known
-    dma_one(p.k, k_off, p.k_st, (q >> 1) ? k1_start(j) : k0_start(j), o, k_voff, q & 1);
+    dma_one(p.k, k_off, p.k_st, (q >> 1) ? k1_start(j) : k0_start(j), o, k_voff, q & 1,
+            __builtin_amdgcn_readlane(tbl, q));
   };
-  auto dma_v = [&](int j, int q) {
+  auto dma_v = [&](int j, int q, int tbl) {
     const int o = kVRegion + (j & 1) * kStageBytes + (q >> 1) * kTileBytes;
-    dma_one(p.v, v_off, p.v_st, (q >> 1) ? v1_start(j) : v0_start(j), o, v_voff, q & 1);
+    dma_one(p.v, v_off, p.v_st, (q >> 1) ? v1_start(j) : v0_start(j), o, v_voff, q & 1,
+            __builtin_amdgcn_readlane(tbl, 4 + q));
   };
   auto load_stage = [&](int j) {
+    const int tbl = tbl_fetch(j);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dma_k(j, q);
+    for (int q = 0; q < 4; ++q) dma_k(j, q, tbl);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dma_v(j, q);
+    for (int q = 0; q < 4; ++q) dma_v(j, q, tbl);
   };
   // Each wave waits for its own loads, then the barrier publishes them to the work-group.
   // The builtin wait tells the compiler its own loads (Q) are done; the assembly one is the real
@@ -424,9 +445,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   };
 
   // Prologue: stage -1 (slot 1) holds K(0,0) for stream 0's first scores, stage 0 goes to slot 0.
+  int tbl[2] = {0, 0};  // tbl[j & 1]: table entries of stage j + 1, whose loads step j issues
   if (n_steps > 0) {
     load_stage(-1);
     load_stage(0);
+    tbl[0] = tbl_fetch(1);
   }
   // Every path reaches the loop with no vector load in flight (the Q registers included).
   stage_ready();
@@ -441,8 +464,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     // the step into an immediate (the loop below is unrolled by two for that).
     auto step = [&](int j, auto par) {
       constexpr int slot = decltype(par)::value;
-      auto next_v = [&](int q) { dma_v(2 * (j >> 1) + slot + 1, q); };
-      auto next_k = [&](int q) { dma_k(2 * (j >> 1) + slot + 1, q); };
+      auto next_v = [&](int q) { dma_v(2 * (j >> 1) + slot + 1, q, tbl[slot]); };
+      auto next_k = [&](int q) { dma_k(2 * (j >> 1) + slot + 1, q, tbl[slot]); };
       if (active(j)) {
         u32x4 pb[4];
         softmax(j, sa0, sa1, pb);
@@ -457,6 +480,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
 #pragma unroll
         for (int q = 0; q < 4; ++q) next_k(q);
       }
+      tbl[slot ^ 1] = tbl_fetch(2 * (j >> 1) + slot + 2);
       stage_ready();
     };
     int j = 0;
@@ -471,8 +495,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     __syncthreads();
     auto step = [&](int j, auto par) {
       constexpr int slot = decltype(par)::value;
-      auto next_v = [&](int q) { dma_v(2 * (j >> 1) + slot + 1, q); };
-      auto next_k = [&](int q) { dma_k(2 * (j >> 1) + slot + 1, q); };
+      auto next_v = [&](int q) { dma_v(2 * (j >> 1) + slot + 1, q, tbl[slot]); };
+      auto next_k = [&](int q) { dma_k(2 * (j >> 1) + slot + 1, q, tbl[slot]); };
       if (active(j - 1)) {
         pv(slot, pbv, next_v);
       } else {
@@ -487,6 +511,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
 #pragma unroll
         for (int q = 0; q < 4; ++q) next_k(q);
       }
+      tbl[slot ^ 1] = tbl_fetch(2 * (j >> 1) + slot + 2);
       stage_ready();
     };
     int j = 0;
