@@ -1,7 +1,7 @@
 """Benchmark of the MI355X attention hot path; prints one JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary] [--no-e2e]
-                    [--only prefill|decode|ragged|copy|e2e]
+                    [--only prefill|decode|ragged|paged|copy|e2e]
 
 A "step" is one call of the hot path on one batch of synthetic input, inputs resident in HBM:
 
@@ -11,6 +11,8 @@ A "step" is one call of the hot path on one batch of synthetic input, inputs res
       block table -> HBM GB/s (every visible K/V byte once + q, o, block table, lengths), with
       enough pool copies rotated per step that no step finds its K/V in the 256 MB MALL;
       ragged packed prefill, 16 sequences with L ~ U[16, 1024] -> TFLOP/s;
+      paged prefill, the 4096-token causal prompt read through a permuted 16-token block table
+      (the engine's prompt path) -> TFLOP/s;
       end to end, the Qwen2.5-1.5B architecture (random bf16 weights) serving 16 concurrent chats
       (prompts U[32, 1000], 64 tokens each) through the scheduler -> generated tok/s.
 
@@ -81,6 +83,21 @@ def bench_ragged(steps, warmup):
     mx = max(lens)
     ms = _time_gpu(lambda i=0: fa2_varlen(q, k, v, cu_t, cu_t, mx, is_causal=True), steps, warmup)
     return ms, wl.causal_prefill_flops(lens), lens
+
+
+def bench_paged_prefill(steps, warmup, seq_len=4096):
+    """The prefill of a prompt whose K/V are already in the paged cache (the engine's path):
+    1 x 12q/2kv x seq_len causal over 16-token blocks in a permuted order."""
+    import torch
+    import workloads as wl
+    from kernels.fa2 import fa2_paged
+    q, kp, vp, tables = wl.prefill_paged(seq_len, seed=0)
+    q, kp, vp = q.cuda(), kp.cuda(), vp.cuda()
+    bt = wl.table_tensor(tables).cuda()
+    lens = torch.tensor([seq_len], dtype=torch.int32, device="cuda")
+    ms = _time_gpu(lambda i=0: fa2_paged(q, kp, vp, bt, lens, max_kv_len=seq_len, is_causal=True),
+                   steps, warmup)
+    return ms, wl.causal_prefill_flops([seq_len])
 
 
 def bench_decode(steps, warmup, rotate_bytes=2 << 30):
@@ -239,6 +256,9 @@ def run_only(which, steps, warmup):
     elif which == "decode":
         ms, nbytes, _, _ = bench_decode(steps, warmup)
         rate, unit = nbytes / (ms * 1e-3) / 1e9, "GB/s"
+    elif which == "paged":
+        ms, flops = bench_paged_prefill(steps, warmup)
+        rate, unit = flops / (ms * 1e-3) / 1e12, "TFLOP/s"
     elif which == "ragged":
         ms, flops, _ = bench_ragged(steps, warmup)
         rate, unit = flops / (ms * 1e-3) / 1e12, "TFLOP/s"
@@ -268,7 +288,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-secondary", action="store_true", help="prefill headline only")
     ap.add_argument("--no-e2e", action="store_true", help="skip the 16-chat end-to-end run")
-    ap.add_argument("--only", choices=("prefill", "decode", "ragged", "copy", "e2e"),
+    ap.add_argument("--only", choices=("prefill", "decode", "ragged", "paged", "copy", "e2e"),
                     help="run one workload alone (counter profiles)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -336,7 +356,15 @@ def main():
                            f"12q/2kv, head_dim 128, bf16",
                "roofline": {"bound": "mfma", "achieved": round(rt, 2), "peak": PEAK_BF16_TFLOPS,
                             "unit": "TFLOP/s", "frac": round(rt / PEAK_BF16_TFLOPS, 4)}}
-        out["secondary"] = [dec, rag]
+        pms, pflops = bench_paged_prefill(args.steps, args.warmup)
+        pt = pflops / (pms * 1e-3) / 1e12
+        pag = {"metric": "paged prefill attn TFLOP/s", "value": round(pt, 2), "unit": "TFLOP/s",
+               "ms_per_step": round(pms, 5), "flops_per_step": pflops,
+               "workload": "causal prefill, 1 x 12q/2kv x 4096 x 128 bf16, K/V read from the paged "
+                           "pool through a permuted table of 16-token blocks",
+               "roofline": {"bound": "mfma", "achieved": round(pt, 2), "peak": PEAK_BF16_TFLOPS,
+                            "unit": "TFLOP/s", "frac": round(pt / PEAK_BF16_TFLOPS, 4)}}
+        out["secondary"] = [dec, rag, pag]
         if not args.no_e2e:
             out["secondary"].append(e2e_line(bench_e2e()))
     print(json.dumps(out), flush=True)

@@ -62,6 +62,18 @@ def decode_paged(n_rows=64, lo=128, hi=8192, block_size=BLOCK_SIZE, dtype=torch.
     return q, k_pool, v_pool, tables, kv_lens
 
 
+def prefill_paged(seq_len=4096, block_size=BLOCK_SIZE, dtype=torch.bfloat16, seed=0):
+    """One causal prompt whose keys sit in the paged pool, blocks in a random order: q
+    [1, 12, L, 128], k_pool / v_pool [L, 2, 128] (exactly the prompt's blocks), its table."""
+    g = torch.Generator().manual_seed(seed)
+    n_blocks = math.ceil(seq_len / block_size)
+    table = torch.randperm(n_blocks, generator=g).tolist()
+    q = torch.randn(1, NUM_HEADS, seq_len, HEAD_DIM, generator=g).to(dtype)
+    k_pool = torch.randn(n_blocks * block_size, NUM_KV_HEADS, HEAD_DIM, generator=g).to(dtype)
+    v_pool = torch.randn(n_blocks * block_size, NUM_KV_HEADS, HEAD_DIM, generator=g).to(dtype)
+    return q, k_pool, v_pool, [table]
+
+
 def table_tensor(tables, width=None):
     """Per-row block lists -> [B, width] int32, short rows padded with block 0 (kv_cache.py:95)."""
     width = width if width is not None else max(1, max(len(t) for t in tables))

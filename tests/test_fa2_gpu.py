@@ -207,6 +207,21 @@ def test_paged_decode_equals_dense_decode_bitwise():
     assert torch.equal(o_dense.cpu(), o_paged.cpu())
 
 
+def test_paged_prefill_4096_equals_dense_prefill_bitwise():
+    # The bench's paged prefill workload: the same kernel reading K/V through a permuted table of
+    # 16-token blocks must give the dense kernel's bits on the gathered K/V.
+    q, kp, vp, tables = wl.prefill_paged(4096, seed=0)
+    kd = opaged.gather_dense(kp, tables, 4096, 16).contiguous()
+    vd = opaged.gather_dense(vp, tables, 4096, 16).contiguous()
+    lens_t = torch.tensor([4096], dtype=torch.int32, device=DEV)
+    announce("[gpu] paged vs dense prefill 4096 causal")
+    o_dense = FlashAttention2Function.apply(q.to(DEV), kd.to(DEV), vd.to(DEV), True, None)
+    o_paged = fa2_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), wl.table_tensor(tables).to(DEV), lens_t,
+                        max_kv_len=4096, is_causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o_dense.cpu(), o_paged.cpu())
+
+
 def test_paged_prefill_over_cached_context():
     # a new turn of T tokens appended to chats that already hold context (kv_lens include T)
     g = torch.Generator().manual_seed(5)
