@@ -34,13 +34,27 @@ constexpr int kRedPitch = kHeadDim + 4;
 #define MI_FA2_DC_NT 1
 #endif
 
+// Paged mode: the block-table entries of one wave step (keys kb .. kb+31: two 16-token runs), in
+// lanes 0 and 1.  Fetched a step ahead, so a step's K/V loads never wait for a table read.
+template <int MODE>
+__device__ __forceinline__ int dc_tbl_fetch(const FwdParams& p, int b, int kb, int k_end, int lane) {
+  if constexpr (MODE == kPaged) {
+    const int t = kb + 16 * lane;
+    if (lane < 2 && t < k_end)
+      return p.block_table[(int64_t)b * p.bt_stride + (t >> __builtin_ctz(p.block_size))];
+    return -1;
+  } else {
+    return 0;
+  }
+}
+
 template <int MODE>
 __device__ __forceinline__ const uint16_t* dc_run(const FwdParams& p, const uint16_t* base,
-                                                  int64_t off, int64_t st, int b, int t) {
+                                                  int64_t off, int64_t st, int b, int t, int blk) {
   // Pointer to token t (a multiple of 16) of row b; the next 15 tokens follow at stride st.
+  // Paged mode: blk is the table entry of t's block.
   if constexpr (MODE == kPaged) {
     const int bs_shift = __builtin_ctz(p.block_size);
-    const int blk = p.block_table[(int64_t)b * p.bt_stride + (t >> bs_shift)];
     if ((unsigned)blk >= (unsigned)p.num_blocks) return nullptr;
     const int64_t slot = ((int64_t)blk << bs_shift) + (t & (p.block_size - 1));
     return base + off + slot * st;
@@ -71,12 +85,13 @@ struct DcStep {
 
 template <int MODE>
 __device__ __forceinline__ void dc_load(const FwdParams& p, int b, int64_t k_off, int64_t v_off,
-                                        int kb, int k_end, int n, int g, DcStep& s) {
+                                        int kb, int k_end, int n, int g, int tbl, DcStep& s) {
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
     const int t = kb + 16 * hf;
-    const uint16_t* kr = t < k_end ? dc_run<MODE>(p, p.k, k_off, p.k_st, b, t) : nullptr;
-    const uint16_t* vr = t < k_end ? dc_run<MODE>(p, p.v, v_off, p.v_st, b, t) : nullptr;
+    const int blk = __builtin_amdgcn_readlane(tbl, hf);
+    const uint16_t* kr = t < k_end ? dc_run<MODE>(p, p.k, k_off, p.k_st, b, t, blk) : nullptr;
+    const uint16_t* vr = t < k_end ? dc_run<MODE>(p, p.v, v_off, p.v_st, b, t, blk) : nullptr;
     // K as the A operand: lane row n is token t + n, slots cover d = 32*ks + 8*g + [0, 8).
     const bool kok = kr != nullptr && t + n < k_end;
 #pragma unroll
@@ -277,21 +292,27 @@ __global__ __launch_bounds__(256, DcShape<MODE>::kOcc) void fa2_decode_kernel(co
     if constexpr (DcShape<MODE>::kPipe) {
       // Two register buffers: step s+1's loads fly during step s's math.
       DcStep s0, s1;
-      if (kb < k_end) dc_load<MODE>(p, b, k_off, v_off, kb, k_end, n, g, s0);
+      int tbl = dc_tbl_fetch<MODE>(p, b, kb, k_end, lane);
+      if (kb < k_end) dc_load<MODE>(p, b, k_off, v_off, kb, k_end, n, g, tbl, s0);
+      tbl = dc_tbl_fetch<MODE>(p, b, kb + kDcChunk, k_end, lane);
       while (kb < k_end) {
         const int kb1 = kb + kDcChunk;
-        if (kb1 < k_end) dc_load<MODE>(p, b, k_off, v_off, kb1, k_end, n, g, s1);
+        if (kb1 < k_end) dc_load<MODE>(p, b, k_off, v_off, kb1, k_end, n, g, tbl, s1);
+        tbl = dc_tbl_fetch<MODE>(p, b, kb1 + kDcChunk, k_end, lane);
         dc_compute<E>(s0, qb, kb, k_end, g, cl, m_run, l_run, oacc);
         if (kb1 >= k_end) break;
         const int kb2 = kb1 + kDcChunk;
-        if (kb2 < k_end) dc_load<MODE>(p, b, k_off, v_off, kb2, k_end, n, g, s0);
+        if (kb2 < k_end) dc_load<MODE>(p, b, k_off, v_off, kb2, k_end, n, g, tbl, s0);
+        tbl = dc_tbl_fetch<MODE>(p, b, kb2 + kDcChunk, k_end, lane);
         dc_compute<E>(s1, qb, kb1, k_end, g, cl, m_run, l_run, oacc);
         kb = kb2;
       }
     } else {
+      int tbl = dc_tbl_fetch<MODE>(p, b, kb, k_end, lane);
       for (; kb < k_end; kb += kDcChunk) {
         DcStep s0;
-        dc_load<MODE>(p, b, k_off, v_off, kb, k_end, n, g, s0);
+        dc_load<MODE>(p, b, k_off, v_off, kb, k_end, n, g, tbl, s0);
+        tbl = dc_tbl_fetch<MODE>(p, b, kb + kDcChunk, k_end, lane);  // in flight during the math
         dc_compute<E>(s0, qb, kb, k_end, g, cl, m_run, l_run, oacc);
       }
     }
