@@ -9,13 +9,16 @@ gfx950 kernels on torch's current stream:
   * seqlen_q > 1: the MFMA prefill kernel (csrc/fa2_prefill.hip);
   * seqlen_q == 1: the split-KV decode kernel + combine (csrc/fa2_decode.hip).
 
-Two entry points go beyond the reference's padded call:
+Three entry points go beyond the reference's padded call:
 
   * `fa2_paged(q, k_pool, v_pool, block_table, kv_lens, ...)` reads K/V straight out of a
     KVCache-layout pool (kv_cache.py:20-22) through a block table, replacing
     KVCache.read's per-step dense gather (kv_cache.py:117-121) + the padded call.
   * `fa2_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, is_causal)` runs a ragged
     batch packed back to back (no padding).
+  * `fa2_paged_varlen(q, k_pool, v_pool, cu_seqlens_q, block_table, kv_lens, max_seqlen_q, ...)`
+    runs packed rows with different new-token counts over the paged pool in one launch (the
+    prompts of a mixed prefill + decode step).
 
 The HIP kernels cover head_dim 128 in bf16/fp16 (the Qwen2.5-1.5B shape the engine runs).
 Anything else is rejected with an AssertionError, never silently computed another way.
