@@ -538,7 +538,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     dst[65 * 64] = l_run;
   }
   __syncthreads();
-  if (ks == 1 || qrow >= T_b) return;
+  if (ks == 1) return;
+  // Rows past T_b: the packed modes keep their lanes for the row-wise stores below (their values
+  // are merged, harmlessly, and never stored); the other modes are done with them.
+  if constexpr (MODE != kVarlen && MODE != kPagedVarlen) {
+    if (qrow >= T_b) return;
+  }
   {
     const float* src = red + rg * kRedVals * 64 + lane;
     const float m1 = src[64 * 64];
@@ -558,17 +563,44 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   // Accumulator r of d-block db is d = 32*db + 8*(r/4) + 4*g + r%4: four consecutive d per group.
-  uint16_t* op = p.o + o_off + (int64_t)qrow * p.o_st + g * 4;
+  if constexpr (MODE == kVarlen || MODE == kPagedVarlen) {
+    // Packed batches of many short rows: the wave's O rows go through LDS so that every global
+    // store writes whole rows -- row-major [32 rows][128 d] bf16 in this row group's part of the
+    // merge area (already read above; LDS operations of one wave run in order), 16-byte chunks
+    // XOR-swizzled by row % 16 so that the writes (32 rows, one chunk each) and the reads (16
+    // chunks of a row) spread over all banks.  Measured 7% faster on 16 packed sequences; on one
+    // long sequence the round trip lengthens the longest tile and the direct stores below win.
+    uint8_t* ot = reinterpret_cast<uint8_t*>(red + rg * kRedVals * 64);
 #pragma unroll
-  for (int db = 0; db < 4; ++db) {
+    for (int db = 0; db < 4; ++db) {
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const u32x2 val = {E::pack2(oacc[db][rr * 4] * inv, oacc[db][rr * 4 + 1] * inv),
-                         E::pack2(oacc[db][rr * 4 + 2] * inv, oacc[db][rr * 4 + 3] * inv)};
-      *reinterpret_cast<u32x2*>(op + db * 32 + rr * 8) = val;
+      for (int rr = 0; rr < 4; ++rr) {
+        const u32x2 val = {E::pack2(oacc[db][rr * 4] * inv, oacc[db][rr * 4 + 1] * inv),
+                           E::pack2(oacc[db][rr * 4 + 2] * inv, oacc[db][rr * 4 + 3] * inv)};
+        *reinterpret_cast<u32x2*>(ot + r32 * 256 + 16 * ((4 * db + rr) ^ (r32 & 15)) + 8 * g) = val;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {  // rows 4k .. 4k+3, one 16-byte chunk per lane
+      const int row = 4 * k + (lane >> 4), ch = lane & 15;
+      const u32x4 val = *reinterpret_cast<const u32x4*>(ot + row * 256 + 16 * (ch ^ (row & 15)));
+      if (wq0 + row < T_b)
+        *reinterpret_cast<u32x4*>(p.o + o_off + (int64_t)(wq0 + row) * p.o_st + ch * 8) = val;
+    }
+  } else {
+    uint16_t* op = p.o + o_off + (int64_t)qrow * p.o_st + g * 4;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const u32x2 val = {E::pack2(oacc[db][rr * 4] * inv, oacc[db][rr * 4 + 1] * inv),
+                           E::pack2(oacc[db][rr * 4 + 2] * inv, oacc[db][rr * 4 + 3] * inv)};
+        *reinterpret_cast<u32x2*>(op + db * 32 + rr * 8) = val;
+      }
     }
   }
-  if (p.lse && g == 0)
+  if (p.lse && g == 0 && qrow < T_b)
     p.lse[l_off + (int64_t)qrow * p.l_st] =
         l_tot > 0.f ? (m_run + __builtin_log2f(l_tot)) * kLn2 : -INFINITY;
 }
