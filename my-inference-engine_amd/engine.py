@@ -170,8 +170,16 @@ class Engine:
             self.resident.remove(conv)
 
     def _make_room(self, job):
+        """Evict idle conversations, least recently used first, until the job's reservation fits
+        in free blocks (chat.py:128-146) and, for a conversation without cache, a sequence slot is
+        free."""
         busy = {id(j.conv) for j in self.active} | {id(job.conv)}
-        while self.cache.blocks_needed(job.conv.seq, self._reserve_len(job)) > self.cache.free_block_count():
+
+        def short():
+            return (self.cache.blocks_needed(job.conv.seq, self._reserve_len(job))
+                    > self.cache.free_block_count()
+                    or (job.conv.seq is None and self.cache.free_slot_count() == 0))
+        while short():
             idle = [c for c in self.resident if id(c) not in busy]
             if not idle:
                 return False

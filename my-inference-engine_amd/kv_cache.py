@@ -113,7 +113,7 @@ class PackedMeta:
 
 class KVCache:
     def __init__(self, num_blocks, block_size, device, dtype, num_layers, num_kv_heads, head_dim,
-                 *, device_tables=None, max_seqs=256):
+                 *, device_tables=None, max_seqs=None):
         self.buf = torch.zeros(num_layers, 2, num_blocks * block_size, num_kv_heads, head_dim,
                                device=device, dtype=dtype)
         self.num_blocks = num_blocks
@@ -123,42 +123,46 @@ class KVCache:
         self._block_tables = {}   # seq id -> list of block ids, in logical order
         self._lengths = {}        # seq id -> tokens written so far
         self._next_seq = 0
+        # Sequence slots (rows of the device tables).  Every sequence that holds cache holds at
+        # least one block once its first token is written, so num_blocks + a few transient empty
+        # sequences bound how many can be live: with that default the slots never run out first.
+        self.max_seqs = max_seqs if max_seqs is not None else num_blocks + 16
+        self._free_slots = list(range(self.max_seqs - 1, -1, -1))
+        self.slot = {}            # seq id -> slot
         self.device_tables = self.device.type == "cuda" if device_tables is None else device_tables
         if self.device_tables:
             assert self.device.type == "cuda", "device-resident tables need a GPU cache"
-            self.max_seqs = max_seqs
-            self.dev_tables = torch.zeros(max_seqs, num_blocks, dtype=torch.int32, device=device)
-            self.dev_lens = torch.zeros(max_seqs, dtype=torch.int32, device=device)
-            self._free_slots = list(range(max_seqs - 1, -1, -1))
-            self.slot = {}        # seq id -> row of dev_tables / dev_lens
+            self.dev_tables = torch.zeros(self.max_seqs, num_blocks, dtype=torch.int32, device=device)
+            self.dev_lens = torch.zeros(self.max_seqs, dtype=torch.int32, device=device)
 
     # -- bookkeeping (kv_cache.py:31-72) -------------------------------------------------------
     def free_block_count(self):
         return len(self._free_blocks)
+
+    def free_slot_count(self):
+        return len(self._free_slots)
 
     def blocks_needed(self, seq, total_len):
         held = len(self._block_tables[seq]) if seq is not None else 0
         return max(0, math.ceil(total_len / self.block_size) - held)
 
     def alloc(self):
-        if self.device_tables:
-            if not self._free_slots:
-                raise RuntimeError(f"all {self.max_seqs} device table slots are in use")
-            slot = self._free_slots.pop()
+        if not self._free_slots:
+            raise RuntimeError(f"all {self.max_seqs} sequence slots are in use")
+        slot = self._free_slots.pop()
         seq = self._next_seq
         self._next_seq += 1
         self._block_tables[seq] = []
         self._lengths[seq] = 0
+        self.slot[seq] = slot
         if self.device_tables:
-            self.slot[seq] = slot
             self.dev_lens[slot:slot + 1].zero_()
         return seq
 
     def free(self, seq):
         self._free_blocks.extend(self._block_tables.pop(seq))
         del self._lengths[seq]
-        if self.device_tables:
-            self._free_slots.append(self.slot.pop(seq))
+        self._free_slots.append(self.slot.pop(seq))
 
     def length(self, seq):
         return self._lengths[seq]

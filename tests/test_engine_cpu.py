@@ -261,3 +261,20 @@ def test_mixed_and_separate_prefill_generate_the_same_tokens():
         eng.run_until_idle()
         replies.append([j.generated for j in jobs])
     assert replies[0] == replies[1]
+
+
+def test_idle_conversations_are_evicted_when_sequence_slots_run_out():
+    # 64 blocks but only 3 sequence slots: the fourth conversation takes the slot of the least
+    # recently used idle one instead of failing
+    cache = KVCache(64, 16, "cpu", torch.float32, TINY.num_layers, TINY.num_kv_heads, TINY.head_dim,
+                    max_seqs=3)
+    eng = Engine(tiny_model(), cache, max_reply_tokens=2, seed=0)
+    convs = [Conversation() for _ in range(4)]
+    for c in convs:
+        eng.submit(c, list(range(10)), 2)
+        eng.run_until_idle()
+    assert convs[0].seq is None and all(c.seq is not None for c in convs[1:])
+    assert cache.free_slot_count() == 0 and len(cache.slot) == 3
+    job = eng.submit(convs[0], [1, 2], 2)        # re-admitted: evicts convs[1], re-prefills history
+    eng.run_until_idle()
+    assert len(job.generated) == 2 and convs[1].seq is None and convs[0].seq is not None
