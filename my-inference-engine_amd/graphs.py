@@ -33,6 +33,10 @@ class DecodeGraphs:
         self.W = cache.num_blocks
         self.buckets = sorted(buckets)
         self.graphs = {}
+        # One capture stream for all buckets, alive as long as the graphs: the kernels' workspace
+        # is kept per stream, and a stream handle recycled by torch's pool while these graphs
+        # exist would hand their workspace to unrelated calls.
+        self._side = torch.cuda.Stream(device=cache.device)
         for rows in self.buckets:
             self._capture(rows)
 
@@ -65,7 +69,9 @@ class DecodeGraphs:
                               meta.block_table, meta.slot_mapping32)
                 return self.model.forward_meta(ids_dev, cache, meta)
             host = torch.zeros(2 * rows, dtype=torch.int32).pin_memory()
-            bufs = (inp, host)
+            # `out` is written by every replay: it lives as long as the graph (it was allocated
+            # before the capture, so the graph's own memory pool does not hold it)
+            bufs = (inp, host, out)
         else:
             n_meta = 2 * rows + rows * W + rows
             meta_dev = torch.zeros(n_meta, dtype=torch.int32, device=dev)
@@ -81,7 +87,7 @@ class DecodeGraphs:
                 return self.model.forward_meta(ids_dev, cache, meta)
             bufs = (meta_dev, ids_dev, torch.zeros(n_meta, dtype=torch.int32).pin_memory(),
                     torch.zeros(rows, 1, dtype=torch.long).pin_memory())
-        side = torch.cuda.Stream(device=dev)
+        side = self._side
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side), torch.no_grad():
             for _ in range(2):                       # allocations and workspaces happen here
@@ -104,7 +110,7 @@ class DecodeGraphs:
         cache = self.cache
         if cache.device_tables:
             assert len(set(seqs)) == n, "a sequence may appear once per step"
-            inp, host = bufs
+            inp, host, _ = bufs
             for s in seqs:
                 cache.ensure_capacity(s, cache.length(s) + 1)
             h = host.numpy()

@@ -57,6 +57,7 @@ def _envelope(Q, K, V):
 
 
 _WORKSPACES = {}
+_RETIRED = []   # outgrown workspaces: never freed (a captured graph may still use one)
 
 
 def _workspace(nbytes, device):
@@ -64,12 +65,16 @@ def _workspace(nbytes, device):
 
     Its contents need no initialisation (every partial the combine reads is written by the same
     launch), so it is allocated uninitialised -- no fill, which also keeps a captured graph free of
-    memset nodes; one buffer per stream keeps calls on different streams from sharing it."""
+    memset nodes; one buffer per stream keeps calls on different streams from sharing it.  A
+    buffer that is outgrown is kept alive, not freed: a HIP graph captured with it holds its
+    address, and torch keeps alive only the memory a capture itself allocated."""
     if not nbytes:
         return None
     key = (device, torch.cuda.current_stream(device).cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _RETIRED.append(ws)
         ws = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws

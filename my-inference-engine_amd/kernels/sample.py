@@ -15,16 +15,20 @@ from . import _lib
 DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 _WORKSPACES = {}
+_RETIRED = []   # outgrown buffers: never freed (a captured graph may still use one)
 
 
 def _workspace(nbytes, device):
     """The sampler's partials buffer of (device, current stream), grown on demand, uninitialised
-    (every slot the reduction reads is written by the same call)."""
+    (every slot the reduction reads is written by the same call); an outgrown buffer is kept
+    alive, as a graph that captured a call holds its address."""
     if not nbytes:
         return None
     key = (device, torch.cuda.current_stream(device).cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _RETIRED.append(ws)
         ws = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws

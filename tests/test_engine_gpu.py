@@ -154,3 +154,39 @@ def test_engine_mixed_prefill_with_decode_graphs_completes():
     summary = run_concurrent_chats(eng, prompts, reply_tokens=8)
     assert summary["tokens"] == 32
     assert cache.free_block_count() == 128
+
+
+def test_graph_keeps_its_workspace_when_a_later_capture_outgrows_it():
+    """Buckets 1 and 8 are captured on one stream: the larger capture needs a larger split-decode
+    workspace, and the bucket-1 graph, which holds the first workspace's address, must still
+    replay correctly afterwards (an outgrown workspace is kept alive, not freed and reused); and
+    no replay may write into memory allocated after the capture (every buffer a graph writes,
+    its step-metadata output included, lives as long as the graph)."""
+    from graphs import DecodeGraphs
+    g = torch.Generator().manual_seed(9)
+    prompts = [torch.randint(0, SMALL.vocab_size, (1, n), generator=g) for n in (300, 280, 260, 240,
+                                                                                  220, 200, 180, 500)]
+    toks = torch.randint(0, SMALL.vocab_size, (8, 3), generator=g)
+    em, ec = make("cuda", torch.bfloat16, num_blocks=256)
+    gm, gc = make("cuda", torch.bfloat16, num_blocks=256)
+    announce("[gpu] decode graphs: buckets 1 and 8 on one capture stream")
+    graphs = DecodeGraphs(gm, gc, buckets=(1, 8))
+    es = [ec.alloc() for _ in prompts]
+    gs = [gc.alloc() for _ in prompts]
+    with torch.no_grad():
+        for p, a, b in zip(prompts, es, gs):
+            em(p.cuda(), ec, [a])
+            gm(p.cuda(), gc, [b])
+        # churn the allocator so that memory a graph still writes, had it been freed, would be
+        # handed to these tensors (small ones share the pool of the graph's metadata buffers)
+        junk = [torch.full((1 << 20,), float("nan"), device="cuda") for _ in range(16)]
+        junk += [torch.full((2048,), float("nan"), device="cuda") for _ in range(512)]
+        for t, rows in enumerate(([7], list(range(8)), [7])):
+            want = em(toks[rows, t:t + 1].cuda(), ec, [es[i] for i in rows])[:, -1].float()
+            got = graphs.run([gs[i] for i in rows], toks[rows, t].tolist()).float()
+            torch.cuda.synchronize()
+            assert torch.isfinite(got).all() and torch.isfinite(want).all(), t
+            assert (got - want).abs().max().item() <= 0.02 * want.abs().max().item(), t
+        # no replay wrote into memory the graphs do not own
+        assert all(torch.isnan(j).all().item() for j in junk)
+        del junk
