@@ -250,12 +250,15 @@ __device__ __forceinline__ uint32_t perm_b32(uint32_t hi_word, uint32_t lo_word,
 // clamp(x, lo, hi) of a wave-uniform value on the scalar unit (the compiler's clamp pattern is a
 // vector instruction, which then needs a readfirstlane back).
 // x must be wave-uniform; it is passed through readfirstlane so that the operand is an SGPR even
-// where the compiler cannot prove the uniformity itself.
+// where the compiler cannot prove the uniformity itself.  s_max / s_min write SCC, which the
+// compiler may hold live across the statement (the carry of a 64-bit s_add_u32 / s_addc_u32
+// pair), so SCC is declared clobbered.
 __device__ __forceinline__ int sclamp(int x, int lo, int hi) {
   int r;
   asm("s_max_i32 %0, %1, %2\n\ts_min_i32 %0, %0, %3"
       : "=&s"(r)
-      : "s"(__builtin_amdgcn_readfirstlane(x)), "s"(lo), "s"(hi));
+      : "s"(__builtin_amdgcn_readfirstlane(x)), "s"(lo), "s"(hi)
+      : "scc");
   return r;
 }
 

@@ -112,7 +112,13 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   const int ks = wave / kPfRowGroups;
   int b, h, rank;
   if (!prefill_item(blockIdx.x, p.Hkv, p.B * p.Hkv, p.group, n_qt_max, b, h, rank)) return;
-  const int hk = h / p.group;
+  // Work-group constants are made visibly uniform, so that everything derived from them (the load
+  // addresses and sizes issued between the MFMAs) is scalar arithmetic, not VALU work that
+  // competes with the other wave's softmax.
+  b = __builtin_amdgcn_readfirstlane(b);
+  h = __builtin_amdgcn_readfirstlane(h);
+  rank = __builtin_amdgcn_readfirstlane(rank);
+  const int hk = __builtin_amdgcn_readfirstlane(h / p.group);
 
   int T_b, kv_len;
   int64_t q_off, o_off, l_off, k_off, v_off;
@@ -146,6 +152,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     v_off = (MODE == kDense ? (int64_t)b * p.v_sb : 0) + (int64_t)hk * p.v_sh;
   }
 
+  T_b = __builtin_amdgcn_readfirstlane(T_b);
+  kv_len = __builtin_amdgcn_readfirstlane(kv_len);
+  k_off = (int64_t)uniform_u64((uint64_t)k_off);
+  v_off = (int64_t)uniform_u64((uint64_t)v_off);
   const int n_qt = (T_b + kPfRows - 1) / kPfRows;
   const int tile = n_qt - 1 - rank;
   if (tile < 0) return;
@@ -239,9 +249,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     } else {
       // Scalar selects only (no branch in the middle of the MFMA phases that issue these).
       const int t0 = max(ts, 0);
-      int rows = min(kv_hi - ts, kPfBc);
-      rows = ts < 0 ? 0 : rows;
-      rows = max(rows, 0);
+      const int rows = ts < 0 ? 0 : sclamp(kv_hi - ts, 0, kPfBc);
       lds_dma16(uniform_u64(reinterpret_cast<uint64_t>(base + off + (int64_t)t0 * st)),
                 __builtin_amdgcn_readfirstlane(rows * (int)st * 2), lds,
                 voff + h * 32 * (int)st * 2);

@@ -1,0 +1,74 @@
+"""The attention kernels' scalar inline assembly must not break the compiler's 64-bit address
+arithmetic.
+
+A 64-bit scalar add is s_add_u32 (low word, carry out in SCC) followed by s_addc_u32 (high word,
+carry in from SCC).  An inline-assembly statement that writes SCC (s_max_i32, s_min_i32, ...)
+without declaring it clobbered can be scheduled between the two, and the high word then takes the
+statement's SCC as its carry: a load address off by 4 GiB.  This test compiles the kernels for
+gfx950 and checks that the SCC read by every s_addc_u32 / s_subb_u32 was written by the matching
+add / subtract.  Needs hipcc (compile only, no GPU)."""
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+CSRC = Path(__file__).resolve().parents[1] / "my-inference-engine_amd" / "csrc"
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+         "-packed-fp32-ops", "--cuda-device-only", "-S", "-o", "-"]
+
+# scalar instructions that write SCC
+_SCC_WRITERS = re.compile(
+    r"\s+(s_add_u32|s_addc_u32|s_sub_u32|s_subb_u32|s_add_i32|s_sub_i32|s_(max|min)_[iu]32|"
+    r"s_cmp\w*|s_(and|or|xor|andn2|orn2|nand|nor|xnor|not)_b\d+|s_(lshl|lshr)_b\d+|s_ashr_i\d+|"
+    r"s_bfe_\w+|s_abs_i32|s_bcnt\w+|s_lshl\d_add_u32)\b")
+
+
+def carry_hazards(asm):
+    """(line, consumer, scc writer) for every carry consumer whose SCC was last written by an
+    inline-assembly statement (between the compiler's ;;#ASMSTART / ;;#ASMEND markers).  The
+    compiler's own SCC producers (the add of the pair, or an s_cmp it uses as a carry on purpose)
+    are not reported."""
+    lines = asm.split("\n")
+    bad = []
+    for i, line in enumerate(lines):
+        m = re.match(r"\s+(s_addc_u32|s_subb_u32)\b", line)
+        if not m:
+            continue
+        in_asm = False
+        for j in range(i - 1, -1, -1):
+            t = lines[j]
+            if ";;#ASMEND" in t:
+                in_asm = True
+                continue
+            if ";;#ASMSTART" in t:
+                in_asm = False
+                continue
+            if t.startswith(".LBB") or re.match(r"\s+s_cbranch", t):
+                break
+            if _SCC_WRITERS.match(t):
+                if in_asm:
+                    bad.append((i, line.strip(), t.strip()))
+                break
+    return bad
+
+
+def test_checker_flags_a_clobbered_carry():
+    asm = ("\ts_add_u32 s4, s0, s2\n\t;;#ASMSTART\n\ts_max_i32 s6, s7, 0\n\t;;#ASMEND\n"
+           "\ts_addc_u32 s5, s1, s3\n")
+    assert carry_hazards(asm) == [(4, "s_addc_u32 s5, s1, s3", "s_max_i32 s6, s7, 0")]
+    # the compiler's own patterns: the add of the pair, an s_cmp used as a carry, asm without SCC
+    assert carry_hazards("\ts_add_u32 s4, s0, s2\n\t;;#ASMSTART\n\ts_mov_b32 m0, s6\n"
+                         "\t;;#ASMEND\n\ts_addc_u32 s5, s1, s3\n") == []
+    assert carry_hazards("\ts_cmp_lg_u64 s[12:13], 0\n\ts_addc_u32 s15, s15, s16\n") == []
+
+
+@pytest.mark.skipif(not Path(HIPCC).exists(), reason="hipcc not available")
+@pytest.mark.parametrize("src", ["fa2_prefill.hip", "fa2_decode.hip"])
+def test_no_inline_asm_between_a_carry_and_its_use(src):
+    asm = subprocess.run([HIPCC, *FLAGS, str(CSRC / src)], capture_output=True, text=True,
+                         check=True, timeout=600).stdout
+    assert "s_addc_u32" in asm
+    assert carry_hazards(asm) == []
