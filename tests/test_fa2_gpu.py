@@ -172,6 +172,21 @@ def test_paged_decode_64_rows():
     check_close(out, _paged_ref(q, kp, vp, tables, lens, 16, False), what="paged decode")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_paged_decode_few_long_rows(dtype):
+    """Three rows of 15k-24k keys: every (row, kv head) item is spread over about a hundred
+    work-groups, so the split merge runs its loop over more than 16 partials per query head (the
+    64-row case stays under 16).  Also the shape of an engine step with few live chats."""
+    q, kp, vp, tables, lens = wl.decode_paged(n_rows=3, lo=15000, hi=24000, dtype=dtype, seed=11)
+    bt = wl.table_tensor(tables)
+    announce(f"[gpu] paged decode, 3 long rows {lens}, {dtype}")
+    out = fa2_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), bt.to(DEV),
+                    torch.tensor(lens, dtype=torch.int32, device=DEV))
+    torch.cuda.synchronize()
+    check_close(out, _paged_ref(q.float(), kp.float(), vp.float(), tables, lens, 16, False),
+                what="paged decode, long rows")
+
+
 def test_paged_decode_block_permutation_invariance():
     # the same logical rows stored in differently permuted blocks give bit-identical outputs
     q, kp, vp, tables, lens = wl.decode_paged(n_rows=16, lo=1, hi=3000, seed=3, spare_blocks=40)
