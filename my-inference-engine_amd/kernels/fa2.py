@@ -73,9 +73,13 @@ def _workspace(nbytes, device):
     key = (device, torch.cuda.current_stream(device).cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
+        size = int(nbytes)
         if ws is not None:
             _RETIRED.append(ws)
-        ws = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+            # at least double: a workspace that grows step by step (one split more every 128
+            # keys of a growing row) retires O(log) buffers whose sizes sum to less than its own
+            size = max(size, 2 * ws.numel())
+        ws = torch.empty(size, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
 

@@ -405,3 +405,19 @@ def test_workspace_too_small_is_an_error():
                         12, 2, 1, 8192, 128, st(q), st(k), st(k), st(o), None, 0,
                         1 / math.sqrt(128), None, 0, _lib.stream_of(q))
     assert rc == 3 and "workspace" in lib.mi_fa2_last_error().decode()
+
+
+def test_workspace_growth_retires_few_buffers():
+    """A workspace asked for 1, 2, 3, ... 64 MB in turn (a decode batch whose longest row grows)
+    keeps its outgrown buffers alive for captured graphs, but grows by doubling: a handful of
+    retired buffers whose sizes sum to less than the final one, not one per request."""
+    from kernels import fa2 as kfa2
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        before = len(kfa2._RETIRED)
+        for mb in range(1, 65):
+            ws = kfa2._workspace(mb << 20, torch.device(DEV))
+            assert ws.numel() >= mb << 20
+        retired = kfa2._RETIRED[before:]
+    assert len(retired) <= 7, len(retired)
+    assert sum(r.numel() for r in retired) < ws.numel()
