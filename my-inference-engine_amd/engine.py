@@ -192,7 +192,8 @@ class Engine:
         self.resident.append(conv)
 
     def _try_admit_or_defer(self, job):
-        if self.cache.blocks_needed(None, self._reserve_len(job)) > self.cache.num_blocks:
+        if self.cache.blocks_needed(None, self._reserve_len(job)) > min(
+                self.cache.num_blocks, self.cache.max_blocks_per_seq):
             job.rejected = "conversation is too long for the KV cache"
             job.t_done = time.perf_counter()
             self.finished.append(job)

@@ -13,9 +13,9 @@ host-to-device copy per step: the graph itself starts with the metadata launch
 starts, kv_lens, the batch block table and the new tokens' cache slots, and advances the lengths.
 Without device tables the graph reads a host-packed [starts | kv_lens | block_table rows x W |
 slot_mapping rows] buffer (KVCache.pack_step's layout) and the token ids, two copies per step.
-Either way W = the pool's block count, so any sequence fits and the attention kernel's grid and
-workspace (sized for W*block_size keys) never change: its work split follows the actual kv_lens
-on the device.  A batch smaller than its bucket is padded with empty rows (slot -1: no keys,
+Either way W = the most blocks one sequence may hold, so any sequence fits and the attention
+kernel's grid and workspace (sized for W*block_size keys) never change: its work split follows the
+actual kv_lens on the device.  A batch smaller than its bucket is padded with empty rows (slot -1: no keys,
 nothing written to the cache, zeros from attention), whose logits are ignored.
 """
 import numpy as np
@@ -30,7 +30,7 @@ class DecodeGraphs:
         assert cache.device.type == "cuda", "decode graphs need the GPU"
         self.model = model
         self.cache = cache
-        self.W = cache.num_blocks
+        self.W = cache.max_blocks_per_seq
         self.buckets = sorted(buckets)
         self.graphs = {}
         # One capture stream for all buckets, alive as long as the graphs: the kernels' workspace

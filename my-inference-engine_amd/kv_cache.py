@@ -20,8 +20,9 @@ and no per-layer gather happens on the GPU path.  read() (the dense gather) is k
 fallback and for reference-compatible callers.
 
 On the GPU the tables themselves are device-resident (device_tables, the default there): every
-sequence holds a slot with a row of `dev_tables` [max_seqs, num_blocks] int32 and a length in
-`dev_lens` [max_seqs] int32.  A table row is written only when blocks are allocated
+sequence holds a slot with a row of `dev_tables` [max_seqs, max_blocks_per_seq] int32 and a
+length in `dev_lens` [max_seqs] int32 (both bounded independently of the pool size, so the tables
+stay small for a pool of any size: 4096 x 2048 x 4 B = 32 MB at most by default).  A table row is written only when blocks are allocated
 (ensure_capacity: one small copy per allocation), and a step sends only its rows' slots: one HIP
 launch (kernels.meta.step_metadata, csrc/step_meta.hip) derives starts, kv_lens, the batch block
 table, every new token's slot (and positions / last indices for mixed steps) and advances the
@@ -112,8 +113,12 @@ class PackedMeta:
 
 
 class KVCache:
+    # Default cap of one sequence's length: Qwen2.5's context window.
+    DEFAULT_MAX_TOKENS_PER_SEQ = 32768
+    DEFAULT_MAX_SEQS = 4096
+
     def __init__(self, num_blocks, block_size, device, dtype, num_layers, num_kv_heads, head_dim,
-                 *, device_tables=None, max_seqs=None):
+                 *, device_tables=None, max_seqs=None, max_blocks_per_seq=None):
         self.buf = torch.zeros(num_layers, 2, num_blocks * block_size, num_kv_heads, head_dim,
                                device=device, dtype=dtype)
         self.num_blocks = num_blocks
@@ -123,16 +128,25 @@ class KVCache:
         self._block_tables = {}   # seq id -> list of block ids, in logical order
         self._lengths = {}        # seq id -> tokens written so far
         self._next_seq = 0
+        # Blocks one sequence may hold (the width of a device table row): the pool, capped at the
+        # default context length, so the tables do not grow with the square of the pool.
+        if max_blocks_per_seq is None:
+            max_blocks_per_seq = math.ceil(self.DEFAULT_MAX_TOKENS_PER_SEQ / block_size)
+        self.max_blocks_per_seq = max(1, min(num_blocks, max_blocks_per_seq))
         # Sequence slots (rows of the device tables).  Every sequence that holds cache holds at
         # least one block once its first token is written, so num_blocks + a few transient empty
-        # sequences bound how many can be live: with that default the slots never run out first.
-        self.max_seqs = max_seqs if max_seqs is not None else num_blocks + 16
+        # sequences bound how many can be live; the default takes that bound up to 4096 slots (the
+        # scheduler evicts idle conversations when slots run out).
+        if max_seqs is None:
+            max_seqs = min(num_blocks + 16, self.DEFAULT_MAX_SEQS)
+        self.max_seqs = max_seqs
         self._free_slots = list(range(self.max_seqs - 1, -1, -1))
         self.slot = {}            # seq id -> slot
         self.device_tables = self.device.type == "cuda" if device_tables is None else device_tables
         if self.device_tables:
             assert self.device.type == "cuda", "device-resident tables need a GPU cache"
-            self.dev_tables = torch.zeros(self.max_seqs, num_blocks, dtype=torch.int32, device=device)
+            self.dev_tables = torch.zeros(self.max_seqs, self.max_blocks_per_seq, dtype=torch.int32,
+                                          device=device)
             self.dev_lens = torch.zeros(self.max_seqs, dtype=torch.int32, device=device)
 
     # -- bookkeeping (kv_cache.py:31-72) -------------------------------------------------------
@@ -169,6 +183,9 @@ class KVCache:
 
     def ensure_capacity(self, seq, total_len):
         need = self.blocks_needed(seq, total_len)
+        if len(self._block_tables[seq]) + need > self.max_blocks_per_seq:
+            raise RuntimeError(f"seq {seq} would hold {len(self._block_tables[seq]) + need} blocks; "
+                               f"a sequence holds at most {self.max_blocks_per_seq}")
         if need > len(self._free_blocks):
             raise RuntimeError(f"KV cache exhausted: seq {seq} needs {need} more blocks, "
                                f"only {len(self._free_blocks)} free")

@@ -4,6 +4,8 @@ eviction and rejection with tiny block pools.  The model runs its CPU fallback (
 the GPU run of the same model through the HIP kernels is tests/test_engine_gpu.py."""
 import math
 
+import pytest
+
 import torch
 
 from engine import Conversation, Engine, run_concurrent_chats
@@ -278,3 +280,18 @@ def test_idle_conversations_are_evicted_when_sequence_slots_run_out():
     job = eng.submit(convs[0], [1, 2], 2)        # re-admitted: evicts convs[1], re-prefills history
     eng.run_until_idle()
     assert len(job.generated) == 2 and convs[1].seq is None and convs[0].seq is not None
+
+
+def test_table_width_and_slots_are_bounded_independently_of_the_pool():
+    """A sequence holds at most max_blocks_per_seq blocks (default: 32,768 tokens, capped by the
+    pool) and the slot count is capped, so device tables do not grow with the pool's square."""
+    big = KVCache(5000, 16, "cpu", torch.float32, 1, 1, 8)
+    assert big.max_blocks_per_seq == 2048 and big.max_seqs == 4096
+    small = KVCache(100, 16, "cpu", torch.float32, 1, 1, 8)
+    assert small.max_blocks_per_seq == 100 and small.max_seqs == 116
+    c = KVCache(100, 16, "cpu", torch.float32, 1, 1, 8, max_blocks_per_seq=4)
+    s = c.alloc()
+    c.ensure_capacity(s, 64)  # exactly 4 blocks
+    with pytest.raises(RuntimeError, match="at most 4"):
+        c.ensure_capacity(s, 65)
+    assert len(c._block_tables[s]) == 4 and c.free_block_count() == 96
