@@ -204,9 +204,11 @@ __device__ __forceinline__ u32x4 ld16_buf(__amdgpu_buffer_rsrc_t r, int byte_off
 // writes, so it would wait for every such load to finish before the next LDS read of any address
 // (vmcnt(0) in front of the MFMA operand reads of the other stage), serialising the prefetch with
 // the compute it is meant to overlap.  Callers wait with s_waitcnt vmcnt(0) (also as assembly:
-// the compiler drops waits for loads it does not know about) before a barrier.  m0 is written
-// here; the compiler reserves m0 and sets it before every use of its own, so nothing of it is
-// lost.
+// the compiler drops waits for loads it does not know about) before a barrier.  m0 (the LDS
+// destination) is written here without a clobber: the compiler treats m0 as a reserved register
+// and says it ignores clobbers of those.  It does not keep values of its own in m0 either: it
+// writes m0 right before each of its own uses.  tests/test_isa_carry.py checks that in the
+// compiled kernels: no m0 read outside the assembly finds its value set inside it.
 __device__ __forceinline__ void lds_dma16(uint64_t base, uint32_t bytes, uint32_t lds_addr,
                                           int voffset) {
   const u32x4 rsrc = {(uint32_t)base, (uint32_t)(base >> 32) & 0xffffu, bytes, 0x00020000u};

@@ -128,10 +128,14 @@ class KVCache:
         self._block_tables = {}   # seq id -> list of block ids, in logical order
         self._lengths = {}        # seq id -> tokens written so far
         self._next_seq = 0
-        # Blocks one sequence may hold (the width of a device table row): the pool, capped at the
-        # default context length, so the tables do not grow with the square of the pool.
+        self.device_tables = self.device.type == "cuda" if device_tables is None else device_tables
+        # Blocks one sequence may hold.  With device tables this is the width of a table row: the
+        # pool, capped at the default context length, so the tables do not grow with the square
+        # of the pool.  Host tables limit nothing, so there (as in the reference's KVCache) a
+        # sequence may hold the whole pool unless the caller sets a cap.
         if max_blocks_per_seq is None:
-            max_blocks_per_seq = math.ceil(self.DEFAULT_MAX_TOKENS_PER_SEQ / block_size)
+            max_blocks_per_seq = (math.ceil(self.DEFAULT_MAX_TOKENS_PER_SEQ / block_size)
+                                  if self.device_tables else num_blocks)
         self.max_blocks_per_seq = max(1, min(num_blocks, max_blocks_per_seq))
         # Sequence slots (rows of the device tables).  Every sequence that holds cache holds at
         # least one block once its first token is written, so num_blocks + a few transient empty
@@ -142,7 +146,6 @@ class KVCache:
         self.max_seqs = max_seqs
         self._free_slots = list(range(self.max_seqs - 1, -1, -1))
         self.slot = {}            # seq id -> slot
-        self.device_tables = self.device.type == "cuda" if device_tables is None else device_tables
         if self.device_tables:
             assert self.device.type == "cuda", "device-resident tables need a GPU cache"
             self.dev_tables = torch.zeros(self.max_seqs, self.max_blocks_per_seq, dtype=torch.int32,
@@ -183,12 +186,12 @@ class KVCache:
 
     def ensure_capacity(self, seq, total_len):
         need = self.blocks_needed(seq, total_len)
-        if len(self._block_tables[seq]) + need > self.max_blocks_per_seq:
-            raise RuntimeError(f"seq {seq} would hold {len(self._block_tables[seq]) + need} blocks; "
-                               f"a sequence holds at most {self.max_blocks_per_seq}")
         if need > len(self._free_blocks):
             raise RuntimeError(f"KV cache exhausted: seq {seq} needs {need} more blocks, "
                                f"only {len(self._free_blocks)} free")
+        if len(self._block_tables[seq]) + need > self.max_blocks_per_seq:
+            raise RuntimeError(f"seq {seq} would hold {len(self._block_tables[seq]) + need} blocks; "
+                               f"a sequence holds at most {self.max_blocks_per_seq}")
         table = self._block_tables[seq]
         old = len(table)
         for _ in range(need):

@@ -283,10 +283,11 @@ def test_idle_conversations_are_evicted_when_sequence_slots_run_out():
 
 
 def test_table_width_and_slots_are_bounded_independently_of_the_pool():
-    """A sequence holds at most max_blocks_per_seq blocks (default: 32,768 tokens, capped by the
-    pool) and the slot count is capped, so device tables do not grow with the pool's square."""
+    """A sequence holds at most max_blocks_per_seq blocks and the slot count is capped.  The
+    default cap (32,768 tokens) exists only to bound device tables; host tables limit nothing, so
+    there a sequence may hold the whole pool, as in the reference's KVCache."""
     big = KVCache(5000, 16, "cpu", torch.float32, 1, 1, 8)
-    assert big.max_blocks_per_seq == 2048 and big.max_seqs == 4096
+    assert big.max_blocks_per_seq == 5000 and big.max_seqs == 4096
     small = KVCache(100, 16, "cpu", torch.float32, 1, 1, 8)
     assert small.max_blocks_per_seq == 100 and small.max_seqs == 116
     c = KVCache(100, 16, "cpu", torch.float32, 1, 1, 8, max_blocks_per_seq=4)
@@ -295,3 +296,15 @@ def test_table_width_and_slots_are_bounded_independently_of_the_pool():
     with pytest.raises(RuntimeError, match="at most 4"):
         c.ensure_capacity(s, 65)
     assert len(c._block_tables[s]) == 4 and c.free_block_count() == 96
+
+
+def test_long_sequence_on_a_large_host_table_pool_is_accepted():
+    """Host tables (the CPU path, or device_tables=False) accept a sequence longer than the
+    device-table default cap: only the pool running out of blocks refuses it
+    (the reference's kv_cache.py:55-64)."""
+    c = KVCache(3000, 16, "cpu", torch.float32, 1, 1, 8)
+    s = c.alloc()
+    c.ensure_capacity(s, 40000)  # 2,500 blocks: past 32,768 tokens, within the pool
+    assert len(c._block_tables[s]) == 2500 and c.free_block_count() == 500
+    with pytest.raises(RuntimeError, match="exhausted"):
+        c.ensure_capacity(s, 3001 * 16)

@@ -1,12 +1,17 @@
-"""The attention kernels' scalar inline assembly must not break the compiler's 64-bit address
-arithmetic.
+"""The attention kernels' scalar inline assembly must not break the compiler's own register
+use: its 64-bit address arithmetic (SCC) and m0.
 
 A 64-bit scalar add is s_add_u32 (low word, carry out in SCC) followed by s_addc_u32 (high word,
 carry in from SCC).  An inline-assembly statement that writes SCC (s_max_i32, s_min_i32, ...)
 without declaring it clobbered can be scheduled between the two, and the high word then takes the
 statement's SCC as its carry: a load address off by 4 GiB.  This test compiles the kernels for
 gfx950 and checks that the SCC read by every s_addc_u32 / s_subb_u32 was written by the matching
-add / subtract.  Needs hipcc (compile only, no GPU)."""
+add / subtract.
+
+m0 likewise: the LDS-load statement writes m0 (the LDS destination of buffer_load ... lds), which
+the compiler treats as reserved and so cannot be declared clobbered.  The compiler sets m0 right
+before each of its own uses; the check is that every instruction outside the assembly that reads
+m0 finds it last written outside the assembly too.  Needs hipcc (compile only, no GPU)."""
 import re
 import shutil
 import subprocess
@@ -55,6 +60,47 @@ def carry_hazards(asm):
     return bad
 
 
+_M0_WRITE = re.compile(r"\s+\w+\s+m0\s*,")
+# instructions that read m0: an explicit m0 source operand, or an implicit use (LDS-destination
+# loads, messages, relative moves, GWS, interpolation)
+_M0_IMPLICIT = re.compile(r"\s+(s_sendmsg\w*|s_movrel\w*|v_movrel\w*|ds_gws\w*|v_interp\w*)\b"
+                          r"|.*\blds\s*$")
+
+
+def _reads_m0(line):
+    if _M0_IMPLICIT.match(line):
+        return True
+    m = re.match(r"\s+\w+\s+(.*)", line)
+    if not m:
+        return False
+    ops = [o.strip() for o in m.group(1).split(",")]
+    return any(re.search(r"\bm0\b", o) for o in ops[1:])
+
+
+def m0_hazards(asm):
+    """(line, reader, writer) for every m0 read outside the inline assembly whose last m0 write
+    (scanning back through the code) is inside an inline-assembly statement."""
+    lines = asm.split("\n")
+    in_asm = [False] * len(lines)
+    state = False
+    for i, t in enumerate(lines):
+        if ";;#ASMSTART" in t:
+            state = True
+        elif ";;#ASMEND" in t:
+            state = False
+        in_asm[i] = state
+    bad = []
+    for i, line in enumerate(lines):
+        if in_asm[i] or not _reads_m0(line):
+            continue
+        for j in range(i - 1, -1, -1):
+            if _M0_WRITE.match(lines[j]):
+                if in_asm[j]:
+                    bad.append((i, line.strip(), lines[j].strip()))
+                break
+    return bad
+
+
 def test_checker_flags_a_clobbered_carry():
     asm = ("\ts_add_u32 s4, s0, s2\n\t;;#ASMSTART\n\ts_max_i32 s6, s7, 0\n\t;;#ASMEND\n"
            "\ts_addc_u32 s5, s1, s3\n")
@@ -72,3 +118,21 @@ def test_no_inline_asm_between_a_carry_and_its_use(src):
                          check=True, timeout=600).stdout
     assert "s_addc_u32" in asm
     assert carry_hazards(asm) == []
+
+
+def test_checker_flags_m0_set_by_inline_assembly():
+    asm = ("\ts_mov_b32 m0, s2\n\tbuffer_load_dword v1, v2, s[4:7], 0 offen lds\n"
+           "\t;;#ASMSTART\n\ts_mov_b32 m0, s9\n\t;;#ASMEND\n"
+           "\tv_readlane_b32 s3, v4, m0\n\tbuffer_load_dword v1, v2, s[4:7], 0 offen lds\n")
+    assert [b[0] for b in m0_hazards(asm)] == [5, 6]
+    # the compiler resets m0 before its own use: fine; m0 as a destination is not a read
+    assert m0_hazards("\t;;#ASMSTART\n\ts_mov_b32 m0, s9\n\t;;#ASMEND\n\ts_mov_b32 m0, s2\n"
+                      "\tbuffer_load_dword v1, v2, s[4:7], 0 offen lds\n") == []
+
+
+@pytest.mark.skipif(not Path(HIPCC).exists(), reason="hipcc not available")
+@pytest.mark.parametrize("src", ["fa2_prefill.hip", "fa2_decode.hip"])
+def test_no_compiler_m0_read_sees_an_inline_assembly_write(src):
+    asm = subprocess.run([HIPCC, *FLAGS, str(CSRC / src)], capture_output=True, text=True,
+                         check=True, timeout=600).stdout
+    assert m0_hazards(asm) == []
