@@ -66,14 +66,6 @@ class StepMeta:
         bt = self.block_table.to(device).long()
         return bt[:, pos // bs] * bs + pos % bs
 
-    def dense_mask(self, device):
-        """[B, 1, T, S] bottom-right causal mask of the dense fallback (model.py:189-195)."""
-        S = self.max_kv
-        key_pos = torch.arange(S, device=device)
-        starts = torch.tensor(self.starts, device=device)
-        q_pos = starts[:, None] + torch.arange(self.T, device=device)[None, :]
-        return (key_pos[None, None, :] <= q_pos[:, :, None]).unsqueeze(1)
-
 
 @dataclass
 class PackedMeta:

@@ -100,6 +100,26 @@ def repeat_kv(x, n_rep):
     return x[:, :, None].expand(b, h, n_rep, s, d).reshape(b, h * n_rep, s, d)
 
 
+def sdpa_fallback(q, k, v, starts, n_rep):
+    """The reference's CPU attention: fp32 SDPA over repeat_kv-expanded K/V (model.py:104-107)
+    with its mask choice (model.py:181-195).  q [B, Hq, T, d], k/v [B, Hkv, S, d] dense (every row
+    padded to S keys); starts[b]: tokens row b held before this step.  When every row starts at
+    the same place no mask is built: a fresh prefill (start 0) is SDPA's is_causal, whose top-left
+    alignment equals the bottom-right one when T == S, and a one-token step sees every key.
+    Otherwise the explicit [B, 1, T, S] bottom-right mask: query i of row b sees key j iff
+    j <= starts[b] + i."""
+    T, S = q.shape[2], k.shape[2]
+    k, v = repeat_kv(k, n_rep), repeat_kv(v, n_rep)
+    c0 = starts[0]
+    if all(st == c0 for st in starts) and (T == 1 or c0 == 0):
+        return F.scaled_dot_product_attention(q, k, v, is_causal=c0 == 0)
+    key_pos = torch.arange(S, device=q.device)
+    q_pos = (torch.tensor(starts, device=q.device)[:, None]
+             + torch.arange(T, device=q.device)[None, :])
+    mask = (key_pos[None, None, :] <= q_pos[:, :, None]).unsqueeze(1)
+    return F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+
+
 class Attention(nn.Module):
     def __init__(self, cfg):
         super().__init__()
@@ -138,9 +158,7 @@ class Attention(nn.Module):
                 out = self._attend_packed_cpu(q, cache, layer, meta)
                 return self.o_proj(out.transpose(1, 2).reshape(B, T, self.q_size))
             k_all, v_all = cache.read(layer, meta)
-            n_rep = cfg.num_heads // cfg.num_kv_heads
-            out = F.scaled_dot_product_attention(q, repeat_kv(k_all, n_rep), repeat_kv(v_all, n_rep),
-                                                 attn_mask=meta.dense_mask(x.device))
+            out = sdpa_fallback(q, k_all, v_all, meta.starts, cfg.num_heads // cfg.num_kv_heads)
         return self.o_proj(out.transpose(1, 2).reshape(B, T, self.q_size))
 
     def _attend_packed(self, q, cache, layer, meta):

@@ -19,9 +19,10 @@ from oracle import paged as opaged
 pytestmark = pytest.mark.gpu
 
 
-def caches(num_blocks=96, max_seqs=12):
+def caches(num_blocks=96, max_seqs=12, max_blocks_per_seq=None):
     mk = lambda dt: KVCache(num_blocks, 16, "cuda", torch.bfloat16, 1, 2, 128,  # noqa: E731
-                            device_tables=dt, max_seqs=max_seqs)
+                            device_tables=dt, max_seqs=max_seqs,
+                            max_blocks_per_seq=max_blocks_per_seq)
     return mk(False), mk(True)
 
 
@@ -43,17 +44,23 @@ def same_meta(h, d, packed):
         assert torch.equal(h.starts_dev.cpu(), d.starts_dev.cpu())
 
 
-def test_device_metadata_equals_host_metadata_over_a_random_schedule():
+@pytest.mark.parametrize("cap", [None, 8])
+def test_device_metadata_equals_host_metadata_over_a_random_schedule(cap):
+    """cap=8: table rows of 8 blocks over a pool of 96, so the device tables' row stride (8) is
+    narrower than the pool and the step kernel reads them at that stride."""
     random.seed(0)
-    hc, dc = caches()
+    hc, dc = caches(max_blocks_per_seq=cap)
+    if cap:
+        assert dc.dev_tables.shape[1] == cap < dc.num_blocks
+    max_len = (cap or 10**9) * 16
     live = []
-    announce("[gpu] step metadata: random schedule on host vs device tables")
+    announce(f"[gpu] step metadata: random schedule on host vs device tables, cap {cap}")
     for it in range(60):
         op = random.random()
         if len(live) < 2 or (op < 0.25 and len(live) < 10):
             hs, ds = hc.alloc(), dc.alloc()
             assert hs == ds
-            reserve = random.randint(1, 200)
+            reserve = random.randint(1, min(200, max_len))
             if hc.blocks_needed(hs, reserve) <= hc.free_block_count():
                 hc.ensure_capacity(hs, reserve)
                 dc.ensure_capacity(ds, reserve)
@@ -73,7 +80,7 @@ def test_device_metadata_equals_host_metadata_over_a_random_schedule():
         if op < 0.75:
             T = random.choice([1, 1, 1, 3])
             need = sum(hc.blocks_needed(s, hc.length(s) + T) for s in rows)
-            if need > hc.free_block_count():
+            if need > hc.free_block_count() or max(hc.length(s) for s in rows) + T > max_len:
                 continue
             h, d = hc.prepare(rows, T), dc.prepare(rows, T)
             same_meta(h, d, packed=False)
@@ -82,7 +89,8 @@ def test_device_metadata_equals_host_metadata_over_a_random_schedule():
         else:
             counts = [random.choice([1, 1, 2, 17, 40]) for _ in rows]
             need = sum(hc.blocks_needed(s, hc.length(s) + c) for s, c in zip(rows, counts))
-            if need > hc.free_block_count():
+            if need > hc.free_block_count() or any(
+                    hc.length(s) + c > max_len for s, c in zip(rows, counts)):
                 continue
             h, d = hc.prepare_packed(rows, counts), dc.prepare_packed(rows, counts)
             same_meta(h, d, packed=True)
@@ -148,3 +156,60 @@ def test_graphs_on_device_tables_match_host_tables():
         outs.append(torch.stack(steps).cpu())
         assert [cache.length(s) for s in seqs] == [40, 153, 8]
     assert torch.equal(outs[0], outs[1])
+
+
+def _small_model():
+    from model import QwenConfig, Qwen2ForCausalLM
+    cfg = QwenConfig(hidden_size=1536, num_layers=2, num_heads=12, num_kv_heads=2, head_dim=128,
+                     intermediate_size=1024, vocab_size=512)
+    return Qwen2ForCausalLM(cfg).to("cuda").init_random(std=0.02, seed=0).to(torch.bfloat16).eval()
+
+
+def test_graphs_with_tables_narrower_than_the_pool_match_eager_decode():
+    """Decode graphs over a cache whose rows hold at most 8 blocks of a 64-block pool: the graphs
+    are captured at W = 8 (kv capacity 128 keys, not the pool's 1,024), and their logits equal
+    the eager decode's of the same cache state."""
+    from graphs import DecodeGraphs
+    model = _small_model()
+    g = torch.Generator().manual_seed(9)
+    prompts = [torch.randint(0, 512, (1, n), generator=g) for n in (37, 100, 5)]
+    toks = torch.randint(0, 512, (3, 4), generator=g)
+    ec = KVCache(64, 16, "cuda", torch.bfloat16, 2, 2, 128, max_blocks_per_seq=8)
+    gc = KVCache(64, 16, "cuda", torch.bfloat16, 2, 2, 128, max_blocks_per_seq=8)
+    announce("[gpu] decode graphs over 8-block table rows of a 64-block pool")
+    graphs = DecodeGraphs(model, gc, buckets=(2, 4))
+    assert graphs.W == 8
+    es = [ec.alloc() for _ in prompts]
+    gs = [gc.alloc() for _ in prompts]
+    with torch.no_grad():
+        for p, a, b in zip(prompts, es, gs):
+            model(p.cuda(), ec, [a])
+            model(p.cuda(), gc, [b])
+        for t in range(toks.shape[1]):
+            want = model(toks[:, t:t + 1].cuda(), ec, es)[:, -1].float()
+            got = graphs.run(gs, toks[:, t].tolist()).float()
+            torch.cuda.synchronize()
+            assert (got - want).abs().max().item() <= 0.02 * want.abs().max().item(), t
+    assert [gc.length(s) for s in gs] == [41, 104, 9]
+    assert max(len(gc._block_tables[s]) for s in gs) <= 8
+
+
+def test_engine_rejects_a_conversation_past_its_table_row_while_blocks_are_free():
+    from engine import Engine, run_concurrent_chats
+    model = _small_model()
+    cache = KVCache(64, 16, "cuda", torch.bfloat16, 2, 2, 128, max_blocks_per_seq=8)
+    eng = Engine(model, cache, max_reply_tokens=8, seed=0)
+    g = torch.Generator().manual_seed(10)
+    # 100 + 8 + 1 tokens fit 8 blocks (128 tokens); 200 + 8 + 1 need 14 blocks of the 8 a row
+    # may hold, although 64 blocks are free
+    ok, long_ = (torch.randint(0, 512, (n,), generator=g).tolist() for n in (100, 200))
+    announce("[gpu] engine: a conversation longer than its table row")
+    from engine import Conversation
+    c1, c2 = Conversation(), Conversation()
+    j1 = eng.submit(c1, ok, 8)
+    j2 = eng.submit(c2, long_, 8)
+    eng.run_until_idle()
+    torch.cuda.synchronize()
+    assert j2.rejected and "too long" in j2.rejected and not j2.generated
+    assert not j1.rejected and len(j1.generated) == 8
+    assert cache.free_block_count() >= 64 - 8
