@@ -148,6 +148,30 @@ MI_FA2_API int mi_fa2_fwd_paged_varlen(int32_t dtype, const void* q, const void*
                                        int32_t is_causal, float sm_scale, mi_fa2_stream_t stream);
 
 /*
+ * Merge of attention partials over disjoint key ranges.  The reference keeps no partials: its
+ * kernel walks every key of a row in one program (kernels/fa2.py:122-158).  This is the split-KV
+ * reduction of the decode path made callable on its own, for partials that other calls produced:
+ * each partial i of (row r, head h) is what a forward over a sub-range of the row's keys returns,
+ * its normalised output and its log-sum-exp (the O and L of kernels/fa2.py:155-158, L in natural
+ * log), e.g. one per GPU when a long row's keys are spread over several GPUs.  Writes
+ *   lse[r][h] = log sum_i exp(L_i),   o[r][h] = sum_i exp(L_i - lse[r][h]) O_i,
+ * the output and L of one pass over all the keys.  A partial with L_i = -inf saw no key and is
+ * skipped (its O_i is not read); a (row, head) with none left gets o = 0 and lse = -inf.
+ *   part_o [max_parts, n_rows, heads, 128] fp32, part_o_strides: 3 (part, row, head), even;
+ *   part_lse [max_parts, n_rows, heads] fp32, part_lse_strides: 3 (part, row, head);
+ *   n_parts [n_rows] int32 partials used per row (the first n_parts[r]; clamped to
+ *     [0, max_parts]), or NULL: max_parts each;
+ *   o [n_rows, heads, 128] in out_dtype (MI_FA2_BF16, MI_FA2_FP16 or MI_FA2_FP32), o_strides: 2
+ *     (row, head), even; lse [n_rows, heads] fp32 (may be NULL), lse_strides: 2.
+ * n_rows <= 65535 (e.g. batch x query tokens flattened).  No workspace.  Asynchronous on `stream`.
+ */
+MI_FA2_API int mi_fa2_combine(int32_t out_dtype, const float* part_o, const float* part_lse,
+                              const int32_t* n_parts, int32_t n_rows, int32_t heads,
+                              int32_t max_parts, int32_t head_dim, const int64_t* part_o_strides,
+                              const int64_t* part_lse_strides, void* o, const int64_t* o_strides,
+                              float* lse, const int64_t* lse_strides, mi_fa2_stream_t stream);
+
+/*
  * Fused rotary embedding + paged KV-cache write, the step before attention.  Replaces apply_rope
  * (model.py:62-65, applied at model.py:92) and KVCache.write (kv_cache.py:108-115, called at
  * model.py:96) on the GPU path, with bitwise the same results (the reference's 16-bit rounding

@@ -15,6 +15,7 @@ namespace mi_fa2 {
 hipError_t launch_prefill(const FwdParams& p, int dtype, int mode, int max_seqlen_q,
                           hipStream_t stream);
 hipError_t launch_decode(const FwdParams& p, int dtype, int mode, hipStream_t stream);
+hipError_t launch_merge(const MergeParams& p, int out_dtype, hipStream_t stream);
 hipError_t launch_rope_kv(const RopeParams& p, int dtype, hipStream_t stream);
 hipError_t launch_sample(const SampleParams& p, int dtype, hipStream_t stream);
 int sample_chunks(int vocab);
@@ -371,6 +372,51 @@ int mi_fa2_fwd_paged_varlen(int32_t dtype, const void* q, const void* k_pool, co
   p.scale_log2 = sm_scale * mi_fa2::kLog2e;
   return launched(mi_fa2::launch_prefill(p, dtype, mi_fa2::kPagedVarlen, max_seqlen_q,
                                          reinterpret_cast<hipStream_t>(stream)));
+}
+
+int mi_fa2_combine(int32_t out_dtype, const float* part_o, const float* part_lse,
+                   const int32_t* n_parts, int32_t n_rows, int32_t heads, int32_t max_parts,
+                   int32_t head_dim, const int64_t* part_o_strides,
+                   const int64_t* part_lse_strides, void* o, const int64_t* o_strides, float* lse,
+                   const int64_t* lse_strides, mi_fa2_stream_t stream) {
+  if (out_dtype != MI_FA2_BF16 && out_dtype != MI_FA2_FP16 && out_dtype != MI_FA2_FP32)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "out_dtype %d is not bf16 (0), fp16 (1) or fp32 (2)",
+                out_dtype);
+  if (head_dim != mi_fa2::kHeadDim)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "head_dim %d: the kernel is built for head_dim 128",
+                head_dim);
+  if (n_rows < 0 || heads < 0 || max_parts < 0 || n_rows > 65535)
+    return fail(MI_FA2_ERR_INVALID, "bad sizes: n_rows=%d (at most 65535) heads=%d max_parts=%d",
+                n_rows, heads, max_parts);
+  if (n_rows == 0 || heads == 0) return ok();
+  if (!o || !o_strides) return fail(MI_FA2_ERR_INVALID, "o or its strides are NULL");
+  if (lse && !lse_strides) return fail(MI_FA2_ERR_INVALID, "lse strides are NULL");
+  if (max_parts > 0 && (!part_o || !part_lse || !part_o_strides || !part_lse_strides))
+    return fail(MI_FA2_ERR_INVALID, "partials or their strides are NULL");
+  // 8-byte fp32 pairs per lane in, 4 (16-bit) or 8 (fp32) bytes per lane out
+  const uintptr_t out_align = out_dtype == MI_FA2_FP32 ? 8 : 4;
+  if (reinterpret_cast<uintptr_t>(o) % out_align ||
+      (max_parts > 0 && reinterpret_cast<uintptr_t>(part_o) % 8))
+    return fail(MI_FA2_ERR_INVALID, "o or part_o is not aligned for its paired stores / loads");
+  bool even = o_strides[0] % 2 == 0 && o_strides[1] % 2 == 0;
+  for (int i = 0; max_parts > 0 && i < 3; ++i) even = even && part_o_strides[i] % 2 == 0;
+  if (!even) return fail(MI_FA2_ERR_INVALID, "o and part_o strides must be even (element pairs)");
+  mi_fa2::MergeParams p{};
+  p.part_o = part_o;
+  p.part_lse = part_lse;
+  p.n_parts = n_parts;
+  if (max_parts > 0) {
+    p.po_sp = part_o_strides[0], p.po_sr = part_o_strides[1], p.po_sh = part_o_strides[2];
+    p.pl_sp = part_lse_strides[0], p.pl_sr = part_lse_strides[1], p.pl_sh = part_lse_strides[2];
+  }
+  p.o = o;
+  p.o_sr = o_strides[0], p.o_sh = o_strides[1];
+  p.lse = lse;
+  if (lse) p.l_sr = lse_strides[0], p.l_sh = lse_strides[1];
+  p.rows = n_rows;
+  p.heads = heads;
+  p.max_parts = max_parts;
+  return launched(mi_fa2::launch_merge(p, out_dtype, reinterpret_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

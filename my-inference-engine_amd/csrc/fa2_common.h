@@ -168,6 +168,20 @@ struct ModelOpParams {
   float eps;
 };
 
+// Log-sum-exp merge of partials over disjoint key ranges (fa2_merge.hip).  Element strides.
+struct MergeParams {
+  const float* part_o;    // [part][row][head][128] fp32, normalised
+  const float* part_lse;  // [part][row][head] fp32, natural log (-inf: the part saw no key)
+  const int32_t* n_parts; // [rows] partials per row, or NULL: max_parts each
+  int64_t po_sp, po_sr, po_sh;
+  int64_t pl_sp, pl_sr, pl_sh;
+  void* o;                // [row][head][128]
+  int64_t o_sr, o_sh;
+  float* lse;             // [row][head], or NULL
+  int64_t l_sr, l_sh;
+  int32_t rows, heads, max_parts;
+};
+
 // Per-step paged-cache metadata (step_meta.hip).
 struct StepMetaParams {
   const int32_t* row_slots;  // [B] sequence slot of each row, < 0: padding row

@@ -45,6 +45,8 @@ SIGNATURES = {
     "mi_fa2_sample_workspace_size": (_sz, [_i32, _i32]),
     "mi_fa2_sample": (_i32, [_i32, _p, _i64, _i32, _i32, _f32, ctypes.c_uint64, ctypes.c_uint64,
                              _p, _p, _sz, _p]),
+    "mi_fa2_combine": (_i32, [_i32, _p, _p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p,
+                              _p]),
     "mi_fa2_fwd_paged_varlen": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i32, _i32,
                                        _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _i32,
                                        _f32, _p]),

@@ -274,3 +274,41 @@ def fa2_paged_varlen(q, k_pool, v_pool, cu_seqlens_q, block_table, kv_lens, max_
             _strides(q), pool_strides, _strides(O), _strides(L) if L is not None else None,
             int(bool(is_causal)), 1.0 / math.sqrt(d), _lib.stream_of(q)))
     return (O, L) if return_lse else O
+
+
+_OUT_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+def fa2_combine(part_o, part_lse, n_parts=None, out_dtype=torch.bfloat16, return_lse=False):
+    """Merge attention partials computed over disjoint key ranges (mi_fa2_combine).
+
+    part_o   [P, R, H, 128] fp32: partial i of (row r, head h) is the normalised output of a
+             forward over a sub-range of the row's keys
+    part_lse [P, R, H] fp32: its log-sum-exp (natural log, the L of kernels/fa2.py:155-158);
+             -inf: the partial saw no key (its O is not read)
+    n_parts  [R] int32: partials used per row (the first n_parts[r]), or None: all P
+    Returns O [R, H, 128] in out_dtype (and the merged fp32 lse [R, H] if return_lse): what one
+    pass over all the keys gives.
+    """
+    assert part_o.is_cuda and part_lse.is_cuda, "partials must be GPU tensors"
+    assert part_o.dtype == torch.float32 and part_lse.dtype == torch.float32
+    assert part_o.dim() == 4 and part_o.shape[-1] == HEAD_DIM and part_o.stride(-1) == 1
+    P, R, H, d = part_o.shape
+    assert part_lse.shape == (P, R, H), "part_lse is [parts, rows, heads]"
+    assert out_dtype in _OUT_DTYPES, f"out_dtype must be bf16, fp16 or fp32, got {out_dtype}"
+    if n_parts is not None:
+        assert n_parts.dtype == torch.int32 and n_parts.shape == (R,) and n_parts.is_contiguous()
+        assert n_parts.device == part_o.device
+    if any(st % 2 for st in part_o.stride()[:-1]) or part_o.data_ptr() % 8:
+        part_o = part_o.contiguous()
+    O = torch.empty((R, H, d), device=part_o.device, dtype=out_dtype)
+    L = torch.empty((R, H), device=part_o.device, dtype=torch.float32) if return_lse else None
+    lib = _lib.load()
+    with torch.cuda.device(part_o.device):
+        _lib.check(lib.mi_fa2_combine(
+            _OUT_DTYPES[out_dtype], part_o.data_ptr(), part_lse.data_ptr(),
+            n_parts.data_ptr() if n_parts is not None else None, R, H, P, d,
+            _lib.strides(part_o, 3), _lib.strides(part_lse, 3), O.data_ptr(), _lib.strides(O, 2),
+            L.data_ptr() if L is not None else None, _lib.strides(L, 2) if L is not None else None,
+            _lib.stream_of(part_o)))
+    return (O, L) if return_lse else O

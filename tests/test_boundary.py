@@ -22,7 +22,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     names = declared_symbols()
-    assert len(names) == 14
+    assert len(names) == 15
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_lib.SIGNATURES)
@@ -159,3 +159,37 @@ def test_model_ops_reject_bad_arguments():
     assert lib.mi_fa2_silu_mul(0, 16, 100, 16, 64, 2, 64, None) == 1
     assert "gate_up" in lib.mi_fa2_last_error().decode()
     assert lib.mi_fa2_silu_mul(0, 16, 128, 16, 64, 0, 64, None) == 0     # no rows: no-op
+
+
+def _combine(lib, **over):
+    i64 = lambda *v: (ctypes.c_int64 * len(v))(*v)  # noqa: E731
+    a = dict(out_dtype=0, part_o=16, part_lse=16, n_parts=None, n_rows=4, heads=12, max_parts=3,
+             head_dim=128, po=i64(4 * 12 * 128, 12 * 128, 128), pl=i64(48, 12, 1), o=16,
+             os=i64(12 * 128, 128), lse=None, ls=None)
+    a.update(over)
+    return lib.mi_fa2_combine(a["out_dtype"], a["part_o"], a["part_lse"], a["n_parts"],
+                              a["n_rows"], a["heads"], a["max_parts"], a["head_dim"], a["po"],
+                              a["pl"], a["o"], a["os"], a["lse"], a["ls"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(out_dtype=5), 2, "out_dtype"),
+    (dict(head_dim=64), 2, "head_dim"),
+    (dict(n_rows=70000), 1, "65535"),
+    (dict(o=None), 1, "NULL"),
+    (dict(part_o=None), 1, "NULL"),
+    (dict(lse=16), 1, "lse strides"),
+    (dict(o=18), 1, "aligned"),
+    (dict(part_o=20), 1, "aligned"),
+    (dict(os=(ctypes.c_int64 * 2)(12 * 128, 129)), 1, "even"),
+])
+def test_combine_rejects_bad_arguments(over, code, msg):
+    lib = _lib.load()
+    assert _combine(lib, **over) == code
+    assert msg in lib.mi_fa2_last_error().decode()
+
+
+def test_combine_with_nothing_to_do_touches_nothing():
+    lib = _lib.load()
+    assert _combine(lib, n_rows=0, part_o=None, o=None) == 0
+    assert _combine(lib, heads=0, part_o=None, o=None) == 0
