@@ -126,6 +126,30 @@ MI_FA2_API int mi_fa2_fwd_paged(int32_t dtype, const void* q, const void* k_pool
                      mi_fa2_stream_t stream);
 
 /*
+ * The paged forward without a workspace: for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, hosts that forbid hipMalloc).  It has no
+ * counterpart in the reference, whose launcher allocates its outputs per call
+ * (kernels/fa2.py:188-189).  Same arguments, kernels and results as mi_fa2_fwd_paged, minus
+ * workspace / workspace_bytes: the split-decode partials live in a scratch array of 32 MiB
+ * (33,554,432 bytes) that the library holds on every GPU it runs on until the process ends
+ * (e.g. 64 rows x 12 query heads at max_kv_len 8,192 use 25.6 MB).  A call that needs more
+ * (mi_fa2_fwd_paged_workspace_size() above 32 MiB) returns MI_FA2_ERR_WORKSPACE without launching.
+ * The caller still passes every input and output; nothing is allocated or freed, on the device or
+ * the host.  All calls on one GPU share its scratch (its contents need no clearing: every slot
+ * read is written by the same launch), so calls that overlap in time on one GPU, e.g. on two
+ * streams, race: serialise them.
+ */
+MI_FA2_API int mi_fa2_fwd_paged_noalloc(int32_t dtype, const void* q, const void* k_pool,
+                                        const void* v_pool, void* o, float* lse,
+                                        const int32_t* block_table, int64_t block_table_stride,
+                                        const int32_t* kv_lens, int32_t batch, int32_t heads_q,
+                                        int32_t heads_kv, int32_t seqlen_q, int32_t max_kv_len,
+                                        int32_t head_dim, int32_t block_size, int32_t num_blocks,
+                                        const int64_t* q_strides, const int64_t* pool_strides,
+                                        const int64_t* o_strides, const int64_t* lse_strides,
+                                        int32_t is_causal, float sm_scale, mi_fa2_stream_t stream);
+
+/*
  * Packed prefill over the paged cache: several rows, each with its own number of new query tokens,
  * attend to their cached keys in one launch.  The reference has no counterpart: its scheduler runs
  * one un-chunked prompt per forward (chat.py:247-253, model.py:157-199); this entry point lets a

@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 
 #include "fa2_common.h"
 
@@ -141,6 +142,113 @@ void set_lse(FwdParams& p, float* lse, const int64_t* s, int n) {
   }
 }
 
+// Scratch of the no-allocation entry point (mi_fa2_fwd_paged_noalloc): the split-decode
+// workspace as a device array of fixed size, which every GPU the library runs on holds until the
+// process ends.  Host code never passes `scratch` itself to a kernel (on the host that name is a
+// stand-in, not the device address): the address is looked up once per device with
+// hipGetSymbolAddress, with that device current, and kept.  Calls on one GPU share its array, so
+// calls that overlap in time on one GPU (different streams) race.  Nothing in it needs clearing:
+// every partial and count the combine reads is written by the same launch.
+constexpr size_t kScratchBytes = 32u << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  const hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess)
+    return fail(MI_FA2_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "device %d: the scratch table holds %d devices", dev,
+                kMaxDevices);
+  std::call_once(g_scratch_once[dev], [dev] {
+    g_scratch_err[dev] = hipGetSymbolAddress(&g_scratch_ptr[dev], HIP_SYMBOL(scratch));
+  });
+  if (g_scratch_err[dev] != hipSuccess || !g_scratch_ptr[dev])
+    return fail(MI_FA2_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(g_scratch_err[dev]));
+  *out = g_scratch_ptr[dev];
+  return MI_FA2_OK;
+}
+
+// The paged forward behind mi_fa2_fwd_paged (caller's workspace) and mi_fa2_fwd_paged_noalloc
+// (the library's static scratch: use_scratch).
+int fwd_paged(int32_t dtype, const void* q, const void* k_pool, const void* v_pool, void* o,
+              float* lse, const int32_t* block_table, int64_t block_table_stride,
+              const int32_t* kv_lens, int32_t batch, int32_t heads_q, int32_t heads_kv,
+              int32_t seqlen_q, int32_t max_kv_len, int32_t head_dim, int32_t block_size,
+              int32_t num_blocks, const int64_t* q_strides, const int64_t* pool_strides,
+              const int64_t* o_strides, const int64_t* lse_strides, int32_t is_causal,
+              float sm_scale, void* workspace, size_t workspace_bytes, bool use_scratch,
+              mi_fa2_stream_t stream) {
+  if (int rc = check_common(dtype, batch, heads_q, heads_kv, head_dim)) return rc;
+  if (seqlen_q < 0 || max_kv_len < 0)
+    return fail(MI_FA2_ERR_INVALID, "bad lengths: seqlen_q=%d max_kv_len=%d", seqlen_q,
+                max_kv_len);
+  if (block_size < 16 || (block_size & (block_size - 1)))
+    return fail(MI_FA2_ERR_UNSUPPORTED, "block_size %d is not a power of two >= 16", block_size);
+  if (num_blocks < 0) return fail(MI_FA2_ERR_INVALID, "num_blocks %d < 0", num_blocks);
+  if (batch == 0 || seqlen_q == 0) return ok();
+  if (!kv_lens) return fail(MI_FA2_ERR_INVALID, "kv_lens is NULL");
+  if (max_kv_len > 0 && !block_table) return fail(MI_FA2_ERR_INVALID, "block_table is NULL");
+  if (int rc = check_tensor("q", q, q_strides, 3)) return rc;
+  if (int rc = check_tensor("o", o, o_strides, 3)) return rc;
+  if (int rc = check_tensor("k_pool", k_pool, pool_strides, 2)) return rc;
+  if (int rc = check_tensor("v_pool", v_pool, pool_strides, 2)) return rc;
+  if (lse && !lse_strides) return fail(MI_FA2_ERR_INVALID, "lse strides are NULL");
+
+  FwdParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k_pool);
+  p.v = static_cast<const uint16_t*>(v_pool);
+  p.o = static_cast<uint16_t*>(o);
+  p.kv_lens = kv_lens;
+  p.block_table = block_table;
+  p.bt_stride = block_table_stride;
+  p.block_size = block_size;
+  p.num_blocks = num_blocks;
+  p.q_sb = q_strides[0], p.q_sh = q_strides[1], p.q_st = q_strides[2];
+  p.o_sb = o_strides[0], p.o_sh = o_strides[1], p.o_st = o_strides[2];
+  p.k_st = pool_strides[0], p.k_sh = pool_strides[1];
+  p.v_st = pool_strides[0], p.v_sh = pool_strides[1];
+  set_lse(p, lse, lse_strides, 3);
+  p.B = batch;
+  p.Hq = heads_q;
+  p.Hkv = heads_kv;
+  p.group = heads_q / heads_kv;
+  p.T = seqlen_q;
+  p.S = max_kv_len;
+  p.causal = is_causal ? 1 : 0;
+  p.scale_log2 = sm_scale * mi_fa2::kLog2e;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+
+  if (uses_decode(seqlen_q, p.group, batch)) {
+    p.n_wg = decode_work_groups(batch, heads_kv, max_kv_len, true);
+    p.max_splits = decode_splits(max_kv_len);
+    const size_t need = decode_workspace(batch, heads_q, heads_kv, max_kv_len);
+    if (need && use_scratch) {
+      if (need > kScratchBytes)
+        return fail(MI_FA2_ERR_WORKSPACE,
+                    "decode needs %zu scratch bytes; the no-allocation entry point holds at most "
+                    "%zu (use mi_fa2_fwd_paged with a workspace)", need, kScratchBytes);
+      if (int rc = scratch_of_current_device(&workspace)) return rc;
+      workspace_bytes = kScratchBytes;
+    }
+    if (need) {
+      if (!workspace || workspace_bytes < need)
+        return fail(MI_FA2_ERR_WORKSPACE, "decode needs %zu workspace bytes, got %zu", need,
+                    workspace ? workspace_bytes : (size_t)0);
+      set_workspace(p, workspace);
+    }
+    return launched(mi_fa2::launch_decode(p, dtype, mi_fa2::kPaged, s));
+  }
+  return launched(mi_fa2::launch_prefill(p, dtype, mi_fa2::kPaged, seqlen_q, s));
+}
+
 }  // namespace
 
 extern "C" {
@@ -265,60 +373,25 @@ int mi_fa2_fwd_paged(int32_t dtype, const void* q, const void* k_pool, const voi
                      const int64_t* o_strides, const int64_t* lse_strides, int32_t is_causal,
                      float sm_scale, void* workspace, size_t workspace_bytes,
                      mi_fa2_stream_t stream) {
-  if (int rc = check_common(dtype, batch, heads_q, heads_kv, head_dim)) return rc;
-  if (seqlen_q < 0 || max_kv_len < 0)
-    return fail(MI_FA2_ERR_INVALID, "bad lengths: seqlen_q=%d max_kv_len=%d", seqlen_q,
-                max_kv_len);
-  if (block_size < 16 || (block_size & (block_size - 1)))
-    return fail(MI_FA2_ERR_UNSUPPORTED, "block_size %d is not a power of two >= 16", block_size);
-  if (num_blocks < 0) return fail(MI_FA2_ERR_INVALID, "num_blocks %d < 0", num_blocks);
-  if (batch == 0 || seqlen_q == 0) return ok();
-  if (!kv_lens) return fail(MI_FA2_ERR_INVALID, "kv_lens is NULL");
-  if (max_kv_len > 0 && !block_table) return fail(MI_FA2_ERR_INVALID, "block_table is NULL");
-  if (int rc = check_tensor("q", q, q_strides, 3)) return rc;
-  if (int rc = check_tensor("o", o, o_strides, 3)) return rc;
-  if (int rc = check_tensor("k_pool", k_pool, pool_strides, 2)) return rc;
-  if (int rc = check_tensor("v_pool", v_pool, pool_strides, 2)) return rc;
-  if (lse && !lse_strides) return fail(MI_FA2_ERR_INVALID, "lse strides are NULL");
+  return fwd_paged(dtype, q, k_pool, v_pool, o, lse, block_table, block_table_stride, kv_lens,
+                   batch, heads_q, heads_kv, seqlen_q, max_kv_len, head_dim, block_size,
+                   num_blocks, q_strides, pool_strides, o_strides, lse_strides, is_causal,
+                   sm_scale, workspace, workspace_bytes, false, stream);
+}
 
-  FwdParams p{};
-  p.q = static_cast<const uint16_t*>(q);
-  p.k = static_cast<const uint16_t*>(k_pool);
-  p.v = static_cast<const uint16_t*>(v_pool);
-  p.o = static_cast<uint16_t*>(o);
-  p.kv_lens = kv_lens;
-  p.block_table = block_table;
-  p.bt_stride = block_table_stride;
-  p.block_size = block_size;
-  p.num_blocks = num_blocks;
-  p.q_sb = q_strides[0], p.q_sh = q_strides[1], p.q_st = q_strides[2];
-  p.o_sb = o_strides[0], p.o_sh = o_strides[1], p.o_st = o_strides[2];
-  p.k_st = pool_strides[0], p.k_sh = pool_strides[1];
-  p.v_st = pool_strides[0], p.v_sh = pool_strides[1];
-  set_lse(p, lse, lse_strides, 3);
-  p.B = batch;
-  p.Hq = heads_q;
-  p.Hkv = heads_kv;
-  p.group = heads_q / heads_kv;
-  p.T = seqlen_q;
-  p.S = max_kv_len;
-  p.causal = is_causal ? 1 : 0;
-  p.scale_log2 = sm_scale * mi_fa2::kLog2e;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-
-  if (uses_decode(seqlen_q, p.group, batch)) {
-    p.n_wg = decode_work_groups(batch, heads_kv, max_kv_len, true);
-    p.max_splits = decode_splits(max_kv_len);
-    const size_t need = decode_workspace(batch, heads_q, heads_kv, max_kv_len);
-    if (need) {
-      if (!workspace || workspace_bytes < need)
-        return fail(MI_FA2_ERR_WORKSPACE, "decode needs %zu workspace bytes, got %zu", need,
-                    workspace ? workspace_bytes : (size_t)0);
-      set_workspace(p, workspace);
-    }
-    return launched(mi_fa2::launch_decode(p, dtype, mi_fa2::kPaged, s));
-  }
-  return launched(mi_fa2::launch_prefill(p, dtype, mi_fa2::kPaged, seqlen_q, s));
+int mi_fa2_fwd_paged_noalloc(int32_t dtype, const void* q, const void* k_pool,
+                             const void* v_pool, void* o, float* lse, const int32_t* block_table,
+                             int64_t block_table_stride, const int32_t* kv_lens, int32_t batch,
+                             int32_t heads_q, int32_t heads_kv, int32_t seqlen_q,
+                             int32_t max_kv_len, int32_t head_dim, int32_t block_size,
+                             int32_t num_blocks, const int64_t* q_strides,
+                             const int64_t* pool_strides, const int64_t* o_strides,
+                             const int64_t* lse_strides, int32_t is_causal, float sm_scale,
+                             mi_fa2_stream_t stream) {
+  return fwd_paged(dtype, q, k_pool, v_pool, o, lse, block_table, block_table_stride, kv_lens,
+                   batch, heads_q, heads_kv, seqlen_q, max_kv_len, head_dim, block_size,
+                   num_blocks, q_strides, pool_strides, o_strides, lse_strides, is_causal,
+                   sm_scale, nullptr, 0, true, stream);
 }
 
 int mi_fa2_fwd_paged_varlen(int32_t dtype, const void* q, const void* k_pool, const void* v_pool,

@@ -37,6 +37,9 @@ SIGNATURES = {
                                     _i64, _p, _p, _p, _i32, _p]),
     "mi_fa2_fwd_paged": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32,
                                 _i32, _i32, _i32, _i32, _p, _p, _p, _p, _i32, _f32, _p, _sz, _p]),
+    "mi_fa2_fwd_paged_noalloc": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _i64, _p, _i32, _i32, _i32,
+                                        _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _i32, _f32,
+                                        _p]),
     "mi_fa2_step_metadata": (_i32, [_p, _p, _i32, _i32, _p, _i32, _p, _i64, _i32, _i32, _p, _p,
                                     _p, _p, _p, _p, _p]),
     "mi_fa2_add_rmsnorm": (_i32, [_i32, _p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i32, _i32,

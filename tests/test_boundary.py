@@ -22,7 +22,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     names = declared_symbols()
-    assert len(names) == 15
+    assert len(names) == 16
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_lib.SIGNATURES)
@@ -193,3 +193,19 @@ def test_combine_with_nothing_to_do_touches_nothing():
     lib = _lib.load()
     assert _combine(lib, n_rows=0, part_o=None, o=None) == 0
     assert _combine(lib, heads=0, part_o=None, o=None) == 0
+
+
+def test_noalloc_paged_forward_refuses_more_than_its_scratch_before_launching():
+    """mi_fa2_fwd_paged_noalloc holds 32 MiB of scratch: a decode needing more is refused with
+    MI_FA2_ERR_WORKSPACE before anything touches a device (so this runs without a GPU)."""
+    lib = _lib.load()
+    i64 = lambda *v: (ctypes.c_int64 * len(v))(*v)  # noqa: E731
+    # 64 rows x 12 heads at 16,384 keys need 128 splits x 130 x 4 B per (row, head): 51 MB
+    need = lib.mi_fa2_fwd_paged_workspace_size(64, 12, 2, 1, 16384, 128)
+    assert need > 32 << 20
+    rc = lib.mi_fa2_fwd_paged_noalloc(0, 16, 16, 16, 16, None, 16, 1024, 16, 64, 12, 2, 1, 16384,
+                                      128, 16, 65536, i64(1536, 128, 128), i64(256, 128),
+                                      i64(1536, 128, 128), None, 0, 0.088, None)
+    assert rc == 3
+    msg = lib.mi_fa2_last_error().decode()
+    assert "at most 33554432" in msg and str(need) in msg
