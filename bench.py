@@ -1,7 +1,7 @@
 """Benchmark of the MI355X attention hot path; prints one JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary] [--no-e2e]
-                    [--only prefill|decode|ragged|paged|copy|e2e]
+                    [--only prefill|decode|ragged|paged|plumbing|copy|e2e]
 
 A "step" is one call of the hot path on one batch of synthetic input, inputs resident in HBM:
 
@@ -13,13 +13,15 @@ A "step" is one call of the hot path on one batch of synthetic input, inputs res
       ragged packed prefill, 16 sequences with L ~ U[16, 1024] -> TFLOP/s;
       paged prefill, the 4096-token causal prompt read through a permuted 16-token block table
       (the engine's prompt path) -> TFLOP/s;
+      plumbing prefill, 1 x 12q/2kv x 512 causal fp32 (the reference's CPU-fallback case): its
+      bf16 cast on the GPU -> TFLOP/s, the fp32 CPU fallback as its CPU baseline;
       end to end, the Qwen2.5-1.5B architecture (random bf16 weights) serving 16 concurrent chats
       (prompts U[32, 1000], 64 tokens each) through the scheduler -> generated tok/s.
 
 Timing: W untimed warmup steps, then torch.cuda.synchronize(); a HIP event pair on the stream the
 kernels are launched on brackets exactly K steps; synchronize.  The per-launch duration is the
 event time / K.  The CPU baseline is the fp32 SDPA oracle (the reference's fallback path) on the
-same inputs, on this host's cores, median of 5 runs.
+same inputs, on this host's cores (median of 5-21 runs per workload).
 
 --only runs one workload alone (for counter profiles: one kernel family per process); `copy` is a
 1 GiB device-to-device copy of known size, the calibration for the FETCH_SIZE / WRITE_SIZE
@@ -199,17 +201,53 @@ def cpu_prefill_baseline(seq_len=4096, runs=5):
     import workloads as wl
     from oracle import sdpa
     q, k, v = (t.float() for t in wl.prefill_single(seq_len, seed=0))
-    sdpa.attention_ref(q, k, v, True)  # warm up
-    times = []
-    for _ in range(runs):
-        t0 = time.perf_counter()
-        sdpa.attention_ref(q, k, v, True)
-        times.append(time.perf_counter() - t0)
-    sec = statistics.median(times)
+    sec = _median_time(lambda: sdpa.attention_ref(q, k, v, True), runs)
     return wl.causal_prefill_flops([seq_len]) / sec / 1e12, torch.get_num_threads(), sec
 
 
-def cpu_decode_baseline(runs=3):
+def _median_time(fn, runs):
+    fn()  # warm up
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def cpu_ragged_baseline(runs=7):
+    """The reference's CPU path for a ragged batch: fp32 SDPA row by row, each row's causal mask
+    aligned to its end (kernels/test_fa2.py:28-35, model.py:186-195), over the packed rows."""
+    import torch
+    import workloads as wl
+    from oracle import sdpa
+    q, k, v, lens, cu = wl.prefill_ragged(seed=0)
+    q, k, v = q.float(), k.float(), v.float()
+    sec = _median_time(lambda: sdpa.varlen_ref(q, k, v, cu, cu, True), runs)
+    return wl.causal_prefill_flops(lens) / sec / 1e12, torch.get_num_threads(), sec
+
+
+def bench_plumbing(steps, warmup, seq_len=512, cpu_runs=21, cpu=True):
+    """The reference's plumbing case: 1 x 12q/2kv x 512 x 128 causal, fp32 N(0,1) seed 0.  Its
+    own path is the CPU SDPA fallback (model.py:104-107, the is_causal branch of a fresh prefill),
+    timed here on the host; the GPU runs the bf16 cast of the same inputs through
+    FlashAttention2Function.apply."""
+    import torch
+    import workloads as wl
+    from kernels.fa2 import FlashAttention2Function
+    from model import sdpa_fallback
+    q, k, v = wl.prefill_single(seq_len, dtype=torch.float32, seed=0)
+    flops = wl.causal_prefill_flops([seq_len])
+    qb, kb, vb = (t.bfloat16().cuda() for t in (q, k, v))
+    ms = _time_gpu(lambda i=0: FlashAttention2Function.apply(qb, kb, vb, True, None), steps, warmup)
+    out = {"gpu_ms": ms, "flops": flops}
+    if cpu:
+        sec = _median_time(lambda: sdpa_fallback(q, k, v, [0], 6), cpu_runs)
+        out.update(cpu_sec=sec, cpu_threads=torch.get_num_threads())
+    return out
+
+
+def cpu_decode_baseline(runs=5):
     """The reference's CPU decode path: dense gather of every row's blocks (kv_cache.py:117-121)
     then fp32 SDPA per row; a 16-row sample of the 64-row workload."""
     import torch
@@ -226,13 +264,7 @@ def cpu_decode_baseline(runs=3):
         vd = opaged.gather_dense(vp, tables, S, 16)
         return sdpa.attention_ref(q, kd, vd, False, lens)
 
-    run()
-    times = []
-    for _ in range(runs):
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    sec = statistics.median(times)
+    sec = _median_time(run, runs)
     return wl.decode_bytes(lens) / sec / 1e9, torch.get_num_threads(), sec
 
 
@@ -262,6 +294,9 @@ def run_only(which, steps, warmup):
     elif which == "ragged":
         ms, flops, _ = bench_ragged(steps, warmup)
         rate, unit = flops / (ms * 1e-3) / 1e12, "TFLOP/s"
+    elif which == "plumbing":
+        pl = bench_plumbing(steps, warmup, cpu=False)
+        ms, rate, unit = pl["gpu_ms"], pl["flops"] / (pl["gpu_ms"] * 1e-3) / 1e12, "TFLOP/s"
     else:
         ms, nbytes = bench_copy(steps, warmup)
         rate, unit = 2 * nbytes / (ms * 1e-3) / 1e9, "GB/s"
@@ -288,7 +323,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-secondary", action="store_true", help="prefill headline only")
     ap.add_argument("--no-e2e", action="store_true", help="skip the 16-chat end-to-end run")
-    ap.add_argument("--only", choices=("prefill", "decode", "ragged", "paged", "copy", "e2e"),
+    ap.add_argument("--only", choices=("prefill", "decode", "ragged", "paged", "plumbing", "copy",
+                                       "e2e"),
                     help="run one workload alone (counter profiles)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -346,8 +382,9 @@ def main():
             cgbs, cores, sec = cpu_decode_baseline()
             dec["cpu_baseline"] = {"value": round(cgbs, 3), "unit": "GB/s", "cores": cores,
                                    "kind": "port",
-                                   "sample": f"16 of the 64 rows: dense gather + fp32 SDPA, median "
-                                             f"of 3 runs ({sec:.3f} s each)"}
+                                   "sample": f"16 of the 64 rows (their bytes over their time): "
+                                             f"dense gather (kv_cache.py:117-121) + fp32 SDPA, "
+                                             f"median of 5 runs ({sec:.3f} s each)"}
         rms, rflops, rlens = bench_ragged(args.steps, args.warmup)
         rt = rflops / (rms * 1e-3) / 1e12
         rag = {"metric": "ragged varlen prefill attn TFLOP/s", "value": round(rt, 2),
@@ -355,7 +392,15 @@ def main():
                "workload": f"16 packed causal sequences, L ~ U[16,1024] (sum {sum(rlens)}), "
                            f"12q/2kv, head_dim 128, bf16",
                "roofline": {"bound": "mfma", "achieved": round(rt, 2), "peak": PEAK_BF16_TFLOPS,
-                            "unit": "TFLOP/s", "frac": round(rt / PEAK_BF16_TFLOPS, 4)}}
+                            "unit": "TFLOP/s", "frac": round(rt / PEAK_BF16_TFLOPS, 4),
+                            "traffic": read_traffic("fa2_prefill_kernel_varlen")}}
+        if not args.no_cpu:
+            ct, cores, sec = cpu_ragged_baseline()
+            rag["cpu_baseline"] = {"value": round(ct, 4), "unit": "TFLOP/s", "cores": cores,
+                                   "kind": "port",
+                                   "sample": f"the same 16 packed sequences in fp32, SDPA row by "
+                                             f"row with each row's bottom-right mask, median of 7 "
+                                             f"runs ({sec:.4f} s each)"}
         pms, pflops = bench_paged_prefill(args.steps, args.warmup)
         pt = pflops / (pms * 1e-3) / 1e12
         pag = {"metric": "paged prefill attn TFLOP/s", "value": round(pt, 2), "unit": "TFLOP/s",
@@ -364,7 +409,22 @@ def main():
                            "pool through a permuted table of 16-token blocks",
                "roofline": {"bound": "mfma", "achieved": round(pt, 2), "peak": PEAK_BF16_TFLOPS,
                             "unit": "TFLOP/s", "frac": round(pt / PEAK_BF16_TFLOPS, 4)}}
-        out["secondary"] = [dec, rag, pag]
+        pl = bench_plumbing(args.steps, args.warmup, cpu=not args.no_cpu)
+        gt = pl["flops"] / (pl["gpu_ms"] * 1e-3) / 1e12
+        plb = {"metric": "plumbing prefill attn TFLOP/s (bf16 cast on the GPU)", "value": round(gt, 2),
+               "unit": "TFLOP/s", "ms_per_step": round(pl["gpu_ms"], 5), "flops_per_step": pl["flops"],
+               "workload": "causal prefill 1 x 12q/2kv x 512 x 128, fp32 N(0,1) seed 0; the GPU "
+                           "runs its bf16 cast through FlashAttention2Function.apply",
+               "roofline": {"bound": "mfma", "achieved": round(gt, 2), "peak": PEAK_BF16_TFLOPS,
+                            "unit": "TFLOP/s", "frac": round(gt / PEAK_BF16_TFLOPS, 4)}}
+        if "cpu_sec" in pl:
+            plb["cpu_baseline"] = {
+                "value": round(pl["flops"] / pl["cpu_sec"] / 1e12, 4), "unit": "TFLOP/s",
+                "cores": pl["cpu_threads"], "kind": "port",
+                "sample": f"the fp32 original through the model's CPU SDPA fallback (the "
+                          f"reference's own path for this case), median of 21 runs "
+                          f"({pl['cpu_sec'] * 1e3:.2f} ms each)"}
+        out["secondary"] = [dec, rag, pag, plb]
         if not args.no_e2e:
             out["secondary"].append(e2e_line(bench_e2e()))
     print(json.dumps(out), flush=True)
