@@ -278,6 +278,13 @@ __device__ __forceinline__ int sclamp(int x, int lo, int hi) {
   return r;
 }
 
+// x as a value the compiler cannot see through.  Address arithmetic derived from it stays where it
+// is used instead of being hoisted out of a loop and kept live (or spilled) through the loop.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 __device__ __forceinline__ float fmax3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -64,9 +64,17 @@ struct Parity {
 
 // Work-groups are dispatched round-robin over the chip's 8 XCDs (work-group w runs on XCD w % 8),
 // and each XCD has its own L2.  The (row, query head, query tile) of work-group w is chosen so that
-// the query heads sharing one kv head (one class c = (row, kv head)) run on the same XCDs, so an L2
-// holds the K/V of few classes, and so that every XCD walks its tiles longest first with the same
-// mix of causal tile lengths.  rank 0 is a row's last (longest) query tile.
+// the query heads sharing one kv head (one class c = (row, kv head)) and tile run on the same XCD,
+// so one L2 holds their K/V, and so that every XCD walks its tiles longest first with the same
+// mix of tile lengths.  rank 0 is a row's last (longest) query tile.
+//   * classes dividing 8 (one or a few long rows): each class has 8 / classes XCDs of its own, and
+//     every XCD walks its class's tiles rank by rank;
+//   * otherwise (batches of rows, of equal or ragged lengths): the groups (class, rank) are taken
+//     rank-major, group j = rank * stride + c with an odd stride >= classes, and dealt to XCD
+//     j % 8.  The odd stride rotates a class over the XCDs from one rank to the next, so rows of
+//     different lengths spread over all XCDs instead of pinning a class -- and its row's whole
+//     work -- to XCD c % 8 (16 ragged rows of U[16, 1024] tokens: the busiest XCD carried 1.9x
+//     the least busy one's tiles that way).
 constexpr int kXcds = 8;
 
 __host__ __device__ inline int prefill_grid_size(int classes, int group, int n_qt) {
@@ -74,30 +82,31 @@ __host__ __device__ inline int prefill_grid_size(int classes, int group, int n_q
     const int per_xcd = (classes * group * n_qt + kXcds - 1) / kXcds;
     return kXcds * per_xcd;
   }
-  return kXcds * ((classes + kXcds - 1) / kXcds) * group * n_qt;
+  const int stride = classes | 1;
+  return kXcds * ((stride * n_qt + kXcds - 1) / kXcds) * group;
 }
 
 // Returns false for the padding work-groups of the grid.
 __device__ inline bool prefill_item(int w, int Hkv, int classes, int group, int n_qt, int& b,
                                     int& h, int& rank) {
   const int x = w % kXcds, slot = w / kXcds;
-  int c, u;
+  int c;
   if (classes < kXcds && kXcds % classes == 0) {
     const int X = kXcds / classes;  // XCDs per class
     c = x / X;
-    u = slot * X + x % X;
+    const int u = slot * X + x % X;
+    rank = u / group;
+    h = (c % Hkv) * group + u % group;
   } else {
-    const int ncx = (classes - x + kXcds - 1) / kXcds;  // classes x, x + 8, ... live on XCD x
-    if (ncx <= 0) return false;
-    const int per_rank = ncx * group;
-    const int rem = slot % per_rank;
-    c = x + kXcds * (rem / group);
-    u = (slot / per_rank) * group + rem % group;
+    const int stride = classes | 1;
+    const int j = (slot / group) * kXcds + x;  // group, rank-major
+    rank = j / stride;
+    c = j % stride;
+    if (c >= classes) return false;
+    h = (c % Hkv) * group + slot % group;
   }
-  rank = u / group;
   if (rank >= n_qt) return false;
   b = c / Hkv;
-  h = (c % Hkv) * group + u % group;
   return true;
 }
 
@@ -547,11 +556,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   }
   __syncthreads();
   if (ks == 1) return;
-  // Rows past T_b: the packed modes keep their lanes for the row-wise stores below (their values
-  // are merged, harmlessly, and never stored); the other modes are done with them.
-  if constexpr (MODE != kVarlen && MODE != kPagedVarlen) {
-    if (qrow >= T_b) return;
-  }
+  // Rows past T_b keep their lanes for the row-wise stores below (their values are merged,
+  // harmlessly, and never stored).
   {
     const float* src = red + rg * kRedVals * 64 + lane;
     const float m1 = src[64 * 64];
@@ -571,13 +577,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   // Accumulator r of d-block db is d = 32*db + 8*(r/4) + 4*g + r%4: four consecutive d per group.
-  if constexpr (MODE == kVarlen || MODE == kPagedVarlen) {
-    // Packed batches of many short rows: the wave's O rows go through LDS so that every global
-    // store writes whole rows -- row-major [32 rows][128 d] bf16 in this row group's part of the
-    // merge area (already read above; LDS operations of one wave run in order), 16-byte chunks
-    // XOR-swizzled by row % 16 so that the writes (32 rows, one chunk each) and the reads (16
-    // chunks of a row) spread over all banks.  Measured 7% faster on 16 packed sequences; on one
-    // long sequence the round trip lengthens the longest tile and the direct stores below win.
+  // The wave's O rows go through LDS so that every global store writes whole rows: row-major
+  // [32 rows][128 d] in this row group's part of the merge area (already read above; LDS
+  // operations of one wave run in order), 16-byte chunks XOR-swizzled by row % 16 so that the
+  // writes (32 rows, one chunk each) and the reads (16 chunks of a row) spread over all banks.
+  // Direct stores from the MFMA layout write 16 bytes into each of 32 rows per instruction: 7%
+  // slower on 16 packed sequences, 5% slower on 768 equal 1024-key tiles, the same on one
+  // 4096-token sequence.
+  {
     uint8_t* ot = reinterpret_cast<uint8_t*>(red + rg * kRedVals * 64);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
@@ -595,17 +602,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
       const u32x4 val = *reinterpret_cast<const u32x4*>(ot + row * 256 + 16 * (ch ^ (row & 15)));
       if (wq0 + row < T_b)
         *reinterpret_cast<u32x4*>(p.o + o_off + (int64_t)(wq0 + row) * p.o_st + ch * 8) = val;
-    }
-  } else {
-    uint16_t* op = p.o + o_off + (int64_t)qrow * p.o_st + g * 4;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const u32x2 val = {E::pack2(oacc[db][rr * 4] * inv, oacc[db][rr * 4 + 1] * inv),
-                           E::pack2(oacc[db][rr * 4 + 2] * inv, oacc[db][rr * 4 + 3] * inv)};
-        *reinterpret_cast<u32x2*>(op + db * 32 + rr * 8) = val;
-      }
     }
   }
   if (p.lse && g == 0 && qrow < T_b)
