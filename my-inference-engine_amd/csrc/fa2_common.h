@@ -278,6 +278,12 @@ __device__ __forceinline__ int sclamp(int x, int lo, int hi) {
   return r;
 }
 
+// Paged loads of one stage, resolved one instruction per lane: the 64-bit byte address of the
+// instruction's first row (lo, hi) and its byte length.
+struct PagedLoads {
+  uint32_t lo, hi, bytes;
+};
+
 // x as a value the compiler cannot see through.  Address arithmetic derived from it stays where it
 // is used instead of being hoisted out of a loop and kept live (or spilled) through the loop.
 __device__ __forceinline__ int opaque(int x) {

@@ -216,52 +216,49 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   // Stage j (LDS slot j%2) therefore holds V(j,0), K(j+1,0), V(j-1,1) and K(j,1); it is loaded
   // during step j-1, one barrier per step.
   //
-  // Staging.  Every tile is 16 load instructions of 4 rows; wave w issues instructions w and w + 8
-  // of each tile.  Lane l moves row 4i + l/16, LDS chunk l%16, i.e. global chunk
-  // (l%16) ^ swizzle(row); rows 4i and 4(i+8) agree mod 16, so one offset serves both.
-  // The offsets below are relative to the instruction's first row (paged mode) or to the tile's
-  // first row (the other modes, instruction h adds 32 rows).
+  // Staging.  Every tile is 16 load instructions of 4 rows; instruction i moves rows 4i .. 4i+3,
+  // lane l row 4i + l/16 into LDS chunk l%16, i.e. global chunk (l%16) ^ swizzle(row).
+  //   * dense and packed modes: wave w issues instructions w and w + 8 of each tile; rows 4i and
+  //     4(i+8) agree mod 16, so one offset (relative to the tile's first row, instruction h
+  //     adding 32 rows) serves both;
+  //   * paged modes: wave w issues instructions 2w and 2w + 1, rows 8w .. 8w+7 of the tile, which
+  //     lie in one block (blocks are multiples of 16 rows): one table entry and one address serve
+  //     both, and the offsets are relative to row 8w (instruction h adding 4 rows).
   const int lrow = lane >> 4;
-  const int trow = is_paged(MODE) ? lrow : 4 * wave + lrow;
-  const int k_voff = (int)(trow * p.k_st * 2) + 16 * ((lane & 15) ^ ((4 * wave + lrow) & 15));
-  const int v_voff = (int)(trow * p.v_st * 2) + 16 * ((lane & 15) ^ (4 * lrow));
+  int k_voff[2], v_voff[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int row = is_paged(MODE) ? 8 * wave + 4 * h + lrow : 4 * wave + lrow;  // swizzle row
+    const int trow = is_paged(MODE) ? 4 * h + lrow : 4 * wave + lrow;
+    k_voff[h] = (int)(trow * p.k_st * 2) + 16 * ((lane & 15) ^ (row & 15));
+    v_voff[h] = (int)(trow * p.v_st * 2) + 16 * ((lane & 15) ^ (4 * lrow));
+  }
 
   // Load instruction h (0, 1) of this wave for the 64-key tile starting at key ts, whose LDS copy
   // is bytes [lds_off, +16 KB); rows past kv_hi read as zeros.  The scalar work per instruction is
-  // kept small (it competes with the MFMA and softmax instruction streams of the CU's waves):
-  // dense and packed modes use one resource per tile and a per-lane offset per instruction, and
-  // never branch (a tile outside [0, kv_hi) gets a zero-length resource: its loads write zeros that
-  // no active wave reads); paged mode needs one resource per instruction (its 4 rows share a
-  // block, the tile's 64 rows need not) and skips tiles outside [0, kv_hi).
+  // kept small (it competes with the MFMA and softmax instruction streams of the CU's waves), and
+  // no instruction branches: a tile outside [0, kv_hi) gets a zero-length resource, whose loads
+  // write zeros that no active wave reads.  Dense and packed modes use one resource per tile and a
+  // per-lane offset per instruction; paged modes one resource per 8-row pair (its rows share a
+  // block, the tile's 64 rows need not), whose address and length come precomputed, one tile per
+  // lane (PagedLoads): a pair of loads costs three lane reads instead of two 64-bit scalar
+  // address computations from its table entry.
   const uint32_t lds_base = lds_addr_of(smem);
-  auto dma_one = [&](const uint16_t* base, int64_t off, int64_t st, int ts, int lds_off, int voff,
-                     int h, int blk_pre) {
-    const int i = wave + 8 * h;
+  auto dma_one = [&](const uint16_t* base, int64_t off, int64_t st, int ts, int lds_off,
+                     const int (&voff)[2], int h, const PagedLoads& pl, int tl) {
+    const int i = is_paged(MODE) ? 2 * wave + h : wave + 8 * h;
     const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_base + lds_off + 1024 * i);
     if constexpr (is_paged(MODE)) {
-      if (ts < 0 || ts >= kv_hi) return;
-      const int r0 = ts + 4 * i;
-      int n = min(max(kv_hi - r0, 0), 4);
-      const uint16_t* ptr = base;
-      if (n > 0) {
-        const int bs_shift = __builtin_ctz(p.block_size);
-        const int blk = blk_pre;  // table entry of block r0 >> bs_shift, fetched a step ahead
-        if ((unsigned)blk < (unsigned)p.num_blocks)
-          ptr = base + off + (((int64_t)blk << bs_shift) + (r0 & (p.block_size - 1))) * st;
-        else
-          n = 0;
-      }
-      // The row pointer and length are uniform by construction; say so, or the compiler wraps
-      // the load in a loop over distinct lane values.
-      lds_dma16(uniform_u64(reinterpret_cast<uint64_t>(ptr)),
-                __builtin_amdgcn_readfirstlane(n * (int)st * 2), lds, voff);
+      const uint32_t lo = __builtin_amdgcn_readlane(pl.lo, tl);
+      const uint32_t hi = __builtin_amdgcn_readlane(pl.hi, tl);
+      lds_dma16(((uint64_t)hi << 32) | lo, __builtin_amdgcn_readlane(pl.bytes, tl), lds, voff[h]);
     } else {
       // Scalar selects only (no branch in the middle of the MFMA phases that issue these).
       const int t0 = max(ts, 0);
       const int rows = ts < 0 ? 0 : sclamp(kv_hi - ts, 0, kPfBc);
       lds_dma16(uniform_u64(reinterpret_cast<uint64_t>(base + off + (int64_t)t0 * st)),
                 __builtin_amdgcn_readfirstlane(rows * (int)st * 2), lds,
-                voff + h * 32 * (int)st * 2);
+                voff[0] + h * 32 * (int)st * 2);
     }
   };
 
@@ -271,43 +268,67 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   auto v0_start = [&](int j) { return j * kPfStep; };
   auto v1_start = [&](int j) { return (j - 1) * kPfStep + kPfBc; };
 
-  // Paged modes: the block-table entries of this wave's 8 load instructions of stage j, one per
-  // lane (lane q: K instruction q; lane 4 + q: V instruction q; -1 where nothing is loaded).  A
-  // table read is a vector load, and a wait for it would also wait for every LDS load in flight
-  // (the compiler cannot count those), so each stage's entries are fetched during the step before
-  // the one that issues its loads and arrive with that step's own loads.
+  // Paged modes: the block-table entries of this wave's 8-row pairs of the 4 tiles of stage j,
+  // one per lane (lane t: tile t = K0, K1, V0, V1; -1 where nothing is loaded).  A table read is
+  // a vector load, and a wait for it would also wait for every LDS load in flight (the compiler
+  // cannot count those), so each stage's entries are fetched during the step before the one that
+  // issues its loads and arrive with that step's own loads.
   auto tbl_fetch = [&](int j) -> int {
     if constexpr (is_paged(MODE)) {
-      const int t = (lane >> 1) & 3, h = lane & 1;
+      const int t = lane & 3;
       const int ts = t == 0 ? k0_start(j) : t == 1 ? k1_start(j) : t == 2 ? v0_start(j) : v1_start(j);
-      const int r0 = ts + 4 * (wave + 8 * h);
-      if (lane < 8 && ts >= 0 && ts < kv_hi && r0 < kv_hi)
+      const int r0 = ts + 8 * wave;
+      if (lane < 4 && ts >= 0 && ts < kv_hi && r0 < kv_hi)
         return p.block_table[(int64_t)b * p.bt_stride + (r0 >> __builtin_ctz(p.block_size))];
       return -1;
     } else {
       return 0;
     }
   };
+  // Paged modes: the address and byte length of those pairs, lane t computing its own (the same
+  // lane layout): resolved from the entries once they have arrived -- at the start of the step
+  // that issues the loads, after the previous step's wait -- in a few vector instructions for
+  // all 4 at once.  A tile outside [0, kv_hi), an entry outside the pool or rows past kv_hi give
+  // a zero-length load.
+  auto resolve = [&](int j, int entry) -> PagedLoads {
+    PagedLoads r{};
+    if constexpr (is_paged(MODE)) {
+      const int t = lane & 3;
+      const int ts = t == 0 ? k0_start(j) : t == 1 ? k1_start(j) : t == 2 ? v0_start(j) : v1_start(j);
+      const int r0 = ts + 8 * wave;
+      const int n = min(max(kv_hi - r0, 0), 8);
+      const bool kv = t < 2;
+      const int64_t st = kv ? p.k_st : p.v_st;
+      const uint16_t* base = kv ? p.k + k_off : p.v + v_off;
+      const bool ok = (unsigned)entry < (unsigned)p.num_blocks && n > 0 && ts >= 0;
+      const int bs_shift = __builtin_ctz(p.block_size);
+      const uint64_t addr = reinterpret_cast<uint64_t>(
+          base + (((int64_t)(ok ? entry : 0) << bs_shift) + (r0 & (p.block_size - 1))) * st);
+      r.lo = (uint32_t)addr;
+      r.hi = (uint32_t)(addr >> 32);
+      r.bytes = ok ? (uint32_t)(n * st * 2) : 0u;
+    }
+    return r;
+  };
 
   // The 8 load instructions of a wave for stage j (which goes to LDS slot j & 1): 4 for K tiles,
   // 4 for V tiles, q = 2*tile + h.  Inside the key loop they are issued one at a time between the
   // MFMAs of the score and PV phases rather than as a burst.  `tbl` holds stage j's table entries.
-  auto dma_k = [&](int j, int q, int tbl) {
+  auto dma_k = [&](int j, int q, const PagedLoads& pl) {
     const int o = (j & 1) * kStageBytes + (q >> 1) * kTileBytes;  // j & 1 folds when j's parity is known
-    dma_one(p.k, k_off, p.k_st, (q >> 1) ? k1_start(j) : k0_start(j), o, k_voff, q & 1,
-            __builtin_amdgcn_readlane(tbl, q));
+    dma_one(p.k, k_off, p.k_st, (q >> 1) ? k1_start(j) : k0_start(j), o, k_voff, q & 1, pl, q >> 1);
   };
-  auto dma_v = [&](int j, int q, int tbl) {
+  auto dma_v = [&](int j, int q, const PagedLoads& pl) {
     const int o = kVRegion + (j & 1) * kStageBytes + (q >> 1) * kTileBytes;
-    dma_one(p.v, v_off, p.v_st, (q >> 1) ? v1_start(j) : v0_start(j), o, v_voff, q & 1,
-            __builtin_amdgcn_readlane(tbl, 4 + q));
+    dma_one(p.v, v_off, p.v_st, (q >> 1) ? v1_start(j) : v0_start(j), o, v_voff, q & 1, pl,
+            2 + (q >> 1));
   };
   auto load_stage = [&](int j) {
-    const int tbl = tbl_fetch(j);
+    const PagedLoads pl = resolve(j, tbl_fetch(j));
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dma_k(j, q, tbl);
+    for (int q = 0; q < 4; ++q) dma_k(j, q, pl);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dma_v(j, q, tbl);
+    for (int q = 0; q < 4; ++q) dma_v(j, q, pl);
   };
   // Each wave waits for its own loads, then the barrier publishes them to the work-group.
   // The builtin wait tells the compiler its own loads (Q) are done; the assembly one is the real
@@ -481,8 +502,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     // the step into an immediate (the loop below is unrolled by two for that).
     auto step = [&](int j, auto par) {
       constexpr int slot = decltype(par)::value;
-      auto next_v = [&](int q) { dma_v(2 * (j >> 1) + slot + 1, q, tbl[slot]); };
-      auto next_k = [&](int q) { dma_k(2 * (j >> 1) + slot + 1, q, tbl[slot]); };
+      const PagedLoads pl = resolve(2 * (j >> 1) + slot + 1, tbl[slot]);
+      auto next_v = [&](int q) { dma_v(2 * (j >> 1) + slot + 1, q, pl); };
+      auto next_k = [&](int q) { dma_k(2 * (j >> 1) + slot + 1, q, pl); };
       if (active(j)) {
         u32x4 pb[4];
         softmax(j, sa0, sa1, pb);
@@ -512,8 +534,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     __syncthreads();
     auto step = [&](int j, auto par) {
       constexpr int slot = decltype(par)::value;
-      auto next_v = [&](int q) { dma_v(2 * (j >> 1) + slot + 1, q, tbl[slot]); };
-      auto next_k = [&](int q) { dma_k(2 * (j >> 1) + slot + 1, q, tbl[slot]); };
+      const PagedLoads pl = resolve(2 * (j >> 1) + slot + 1, tbl[slot]);
+      auto next_v = [&](int q) { dma_v(2 * (j >> 1) + slot + 1, q, pl); };
+      auto next_k = [&](int q) { dma_k(2 * (j >> 1) + slot + 1, q, pl); };
       if (active(j - 1)) {
         pv(slot, pbv, next_v);
       } else {
