@@ -62,6 +62,15 @@ bool uses_decode(int64_t seqlen_q, int64_t group, int64_t batch) {
   return seqlen_q == 1 && group <= 16 && batch <= kMaxDecodeBatch;
 }
 
+// The decode kernel reads a 16-token run through a buffer resource of 32-bit byte offsets.
+int check_decode_strides(const FwdParams& p) {
+  const int64_t lim = int64_t(1) << 26;  // 16 rows x 2 bytes x stride < 2^31
+  if (p.k_st < 0 || p.v_st < 0 || p.k_st >= lim || p.v_st >= lim)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "k/v token strides %lld / %lld: at most 2^26 - 1 elements",
+                (long long)p.k_st, (long long)p.v_st);
+  return MI_FA2_OK;
+}
+
 int decode_work_groups(int64_t batch, int64_t heads_kv, int64_t max_kv, bool paged) {
   static const int forced = [] {
     const char* env = std::getenv("MI_FA2_DECODE_WGS");
@@ -244,6 +253,7 @@ int fwd_paged(int32_t dtype, const void* q, const void* k_pool, const void* v_po
                     workspace ? workspace_bytes : (size_t)0);
       set_workspace(p, workspace);
     }
+    if (int rc = check_decode_strides(p)) return rc;
     return launched(mi_fa2::launch_decode(p, dtype, mi_fa2::kPaged, s));
   }
   return launched(mi_fa2::launch_prefill(p, dtype, mi_fa2::kPaged, seqlen_q, s));
@@ -316,6 +326,7 @@ int mi_fa2_fwd(int32_t dtype, const void* q, const void* k, const void* v, void*
                     workspace ? workspace_bytes : (size_t)0);
       set_workspace(p, workspace);
     }
+    if (int rc = check_decode_strides(p)) return rc;
     return launched(mi_fa2::launch_decode(p, dtype, mi_fa2::kDense, s));
   }
   return launched(mi_fa2::launch_prefill(p, dtype, mi_fa2::kDense, seqlen_q, s));

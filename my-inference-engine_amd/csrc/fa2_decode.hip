@@ -30,10 +30,6 @@ constexpr int kDcWaves = 4;
 constexpr int kDcStep = 32;   // keys per wave step
 constexpr int kRedPitch = kHeadDim + 4;
 
-#ifndef MI_FA2_DC_NT
-#define MI_FA2_DC_NT 1
-#endif
-
 // Paged mode: the block-table entries of one wave step (keys kb .. kb+31: two 16-token runs), in
 // lanes 0 and 1.  Fetched a step ahead, so a step's K/V loads never wait for a table read.
 template <int MODE>
@@ -68,14 +64,11 @@ __device__ __forceinline__ uint32_t pick16(uint32_t x, uint32_t y, bool hi) {
   return hi ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
 }
 
-// Streaming 16-byte load of K/V (MI_FA2_DC_NT=1 marks it non-temporal).
-__device__ __forceinline__ u32x4 ld16_kv(const uint16_t* ptr) {
-#if MI_FA2_DC_NT
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ptr));
-#else
-  return ld16(ptr);
+// Cache policy of the K/V loads: non-temporal (streamed once; MI_FA2_DC_NT=0 turns it off).
+#ifndef MI_FA2_DC_NT
+#define MI_FA2_DC_NT 1
 #endif
-}
+constexpr int kDcLoadPolicy = MI_FA2_DC_NT ? 2 : 0;
 
 // One wave step's operands: K in A layout, V rows for the in-register transpose.
 struct DcStep {
@@ -83,6 +76,9 @@ struct DcStep {
   u32x4 va[2][4];
 };
 
+// A 16-token run is read through a buffer resource that ends at the run's last valid token: rows
+// past k_end (and a whole run past it, or a table entry outside the pool) read as zeros with no
+// per-lane condition around the loads.
 template <int MODE>
 __device__ __forceinline__ void dc_load(const FwdParams& p, int b, int64_t k_off, int64_t v_off,
                                         int kb, int k_end, int n, int g, int tbl, DcStep& s) {
@@ -90,20 +86,21 @@ __device__ __forceinline__ void dc_load(const FwdParams& p, int b, int64_t k_off
   for (int hf = 0; hf < 2; ++hf) {
     const int t = kb + 16 * hf;
     const int blk = __builtin_amdgcn_readlane(tbl, hf);
-    const uint16_t* kr = t < k_end ? dc_run<MODE>(p, p.k, k_off, p.k_st, b, t, blk) : nullptr;
-    const uint16_t* vr = t < k_end ? dc_run<MODE>(p, p.v, v_off, p.v_st, b, t, blk) : nullptr;
+    const int rows = t < k_end ? min(k_end - t, 16) : 0;
+    const uint16_t* kr = rows ? dc_run<MODE>(p, p.k, k_off, p.k_st, b, t, blk) : nullptr;
+    const uint16_t* vr = rows ? dc_run<MODE>(p, p.v, v_off, p.v_st, b, t, blk) : nullptr;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kr ? kr : p.k, kr ? rows * (int)p.k_st * 2 : 0);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vr ? vr : p.v, vr ? rows * (int)p.v_st * 2 : 0);
     // K as the A operand: lane row n is token t + n, slots cover d = 32*ks + 8*g + [0, 8).
-    const bool kok = kr != nullptr && t + n < k_end;
+    const int ko = (n * (int)p.k_st + g * 8) * 2;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
-      s.ka[hf][ks] = kok ? ld16_kv(kr + (int64_t)n * p.k_st + ks * 32 + g * 8) : u32x4{0, 0, 0, 0};
+      s.ka[hf][ks] = __builtin_amdgcn_raw_buffer_load_b128(rk, ko + ks * 64, 0, kDcLoadPolicy);
     // V rows for the V^T A operand: token t + 4g + r, dims 8n .. 8n+7.
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tok = 4 * g + r;
-      const bool vok = vr != nullptr && t + tok < k_end;
-      s.va[hf][r] = vok ? ld16_kv(vr + (int64_t)tok * p.v_st + n * 8) : u32x4{0, 0, 0, 0};
-    }
+    for (int r = 0; r < 4; ++r)
+      s.va[hf][r] = __builtin_amdgcn_raw_buffer_load_b128(
+          rv, ((4 * g + r) * (int)p.v_st + n * 8) * 2, 0, kDcLoadPolicy);
   }
 }
 

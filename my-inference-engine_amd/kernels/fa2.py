@@ -198,11 +198,12 @@ def fa2_paged(q, k_pool, v_pool, block_table, kv_lens, *, block_size=16, max_kv_
 
 
 def fa2_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, is_causal=False,
-               return_lse=False):
+               return_lse=False, out=None):
     """Attention over a ragged batch packed back to back.
 
     q [total_q, Hq, 128], k/v [total_k, Hkv, 128]; cu_seqlens_q/k [B+1] int32 prefix offsets;
     row b = q[cu_q[b]:cu_q[b+1]] against k/v[cu_k[b]:cu_k[b+1]], causal aligned to the row's end.
+    out: optional [total_q, Hq, 128] output (any token/head strides, 16-byte aligned).
     Returns O [total_q, Hq, 128] (and the fp32 LSE [Hq, total_q] if return_lse).
     """
     assert q.is_cuda and k.is_cuda and v.is_cuda, "q, k and v must be GPU tensors"
@@ -215,7 +216,8 @@ def fa2_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, is_causal=Fals
     assert Hq % Hkv == 0, "query heads must be a multiple of kv heads (GQA)"
     _envelope(q, k, v)
     q, k, v = _vec(q), _vec(k), _vec(v)
-    O = torch.empty((total_q, Hq, d), device=q.device, dtype=q.dtype)
+    O = out if out is not None else torch.empty((total_q, Hq, d), device=q.device, dtype=q.dtype)
+    assert O.shape == q.shape and O.dtype == q.dtype and _dims_ok(O)
     L = torch.empty((Hq, total_q), device=q.device, dtype=torch.float32)
     lib = _lib.load()
     with torch.cuda.device(q.device):

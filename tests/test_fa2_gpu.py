@@ -137,6 +137,31 @@ def test_ragged_varlen_prefill():
     check_close(out, sdpa.varlen_ref(q, k, v, cu, cu, True), what="varlen")
 
 
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+def test_varlen_every_tile_is_written_for_any_row_count(causal):
+    """Rows x kv heads (the work-group classes) of every count, dividing 8 or not, ragged lengths
+    from 1 to 700 (empty rows too): each output row is written exactly as the oracle's.  The
+    output starts as NaN, so a tile the grid misses fails the finite check."""
+    g = torch.Generator().manual_seed(21)
+    for B in (1, 3, 4, 5, 7, 9, 13, 21):
+        lens = torch.randint(1, 701, (B,), generator=g).tolist()
+        if B > 3:
+            lens[2] = 0
+        cu = [0]
+        for n in lens:
+            cu.append(cu[-1] + n)
+        q = torch.randn(cu[-1], 12, 128, generator=g).to(torch.bfloat16)
+        k = torch.randn(cu[-1], 2, 128, generator=g).to(torch.bfloat16)
+        v = torch.randn(cu[-1], 2, 128, generator=g).to(torch.bfloat16)
+        cu_t = torch.tensor(cu, dtype=torch.int32, device=DEV)
+        out = torch.full((cu[-1], 12, 128), float("nan"), dtype=torch.bfloat16, device=DEV)
+        announce(f"[gpu] varlen tiles B={B} causal={causal}")
+        fa2_varlen(q.to(DEV), k.to(DEV), v.to(DEV), cu_t, cu_t, max(lens), is_causal=causal,
+                   out=out)
+        torch.cuda.synchronize()
+        check_close(out, sdpa.varlen_ref(q, k, v, cu, cu, causal), what=f"B={B}")
+
+
 def test_varlen_with_longer_keys_than_queries():
     # chunked prefill rows: each row's queries are the last T_b of its kv_b keys
     g = torch.Generator().manual_seed(2)
