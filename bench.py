@@ -408,7 +408,8 @@ def main():
                "workload": "causal prefill, 1 x 12q/2kv x 4096 x 128 bf16, K/V read from the paged "
                            "pool through a permuted table of 16-token blocks",
                "roofline": {"bound": "mfma", "achieved": round(pt, 2), "peak": PEAK_BF16_TFLOPS,
-                            "unit": "TFLOP/s", "frac": round(pt / PEAK_BF16_TFLOPS, 4)}}
+                            "unit": "TFLOP/s", "frac": round(pt / PEAK_BF16_TFLOPS, 4),
+                            "traffic": read_traffic("fa2_prefill_kernel_paged")}}
         pl = bench_plumbing(args.steps, args.warmup, cpu=not args.no_cpu)
         gt = pl["flops"] / (pl["gpu_ms"] * 1e-3) / 1e12
         plb = {"metric": "plumbing prefill attn TFLOP/s (bf16 cast on the GPU)", "value": round(gt, 2),
