@@ -86,32 +86,69 @@ __host__ __device__ inline int prefill_grid_size(int classes, int group, int n_q
   return kXcds * ((stride * n_qt + kXcds - 1) / kXcds) * group;
 }
 
-// Returns false for the padding work-groups of the grid.
-__device__ inline bool prefill_item(int w, int Hkv, int classes, int group, int n_qt, int& b,
-                                    int& h, int& rank) {
-  const int x = w % kXcds, slot = w / kXcds;
-  int c;
+// Division by a divisor fixed for the launch, as a multiply: n / d = umulhi(n, m) >> l with
+// l = floor(log2 d) and m = floor(2^(32+l) / d) + 1, exact for n < 2^31 (the error term n*(m*d -
+// 2^(32+l)) / (d*2^(32+l)) < n / 2^(32+l) stays below 1/d); m = 0 marks a power of two (n >> l).
+// The work-group's item is found at its start, before any load can be issued, and the runtime
+// integer divisions this replaces cost a few hundred dependent instructions (1-3% on grids of many
+// short tiles).
+struct FastDiv {
+  uint32_t m, l, d;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f{0, 0, d};
+  while ((2u << f.l) <= d && f.l < 31) ++f.l;
+  if ((d & (d - 1)) != 0) f.m = (uint32_t)(((uint64_t)1 << (32 + f.l)) / d + 1);
+  return f;
+}
+__device__ __forceinline__ int fdiv(int n, const FastDiv& f) {
+  return (int)(f.m ? __umulhi((uint32_t)n, f.m) >> f.l : (uint32_t)n >> f.l);
+}
+
+// The launch's item map: the divisors of prefill_item and, when the classes divide the XCDs,
+// log2 of the XCDs per class (else -1).
+struct ItemMap {
+  FastDiv group, stride, hkv;
+  int32_t classes, xcd_shift;
+};
+inline ItemMap make_item_map(int classes, int group, int Hkv) {
+  ItemMap m{make_fastdiv(group), make_fastdiv(classes | 1), make_fastdiv(Hkv), classes, -1};
   if (classes < kXcds && kXcds % classes == 0) {
-    const int X = kXcds / classes;  // XCDs per class
-    c = x / X;
-    const int u = slot * X + x % X;
-    rank = u / group;
-    h = (c % Hkv) * group + u % group;
+    m.xcd_shift = 0;
+    while ((classes << m.xcd_shift) < kXcds) ++m.xcd_shift;
+  }
+  return m;
+}
+
+// Returns false for the padding work-groups of the grid.
+__device__ inline bool prefill_item(int w, const ItemMap& map, int n_qt, int& b, int& h,
+                                    int& rank) {
+  const int x = w % kXcds, slot = w / kXcds;
+  const int group = (int)map.group.d;
+  int c;
+  if (map.xcd_shift >= 0) {
+    const int X = 1 << map.xcd_shift;  // XCDs per class
+    c = x >> map.xcd_shift;
+    const int u = slot * X + (x & (X - 1));
+    rank = fdiv(u, map.group);
+    h = (c - fdiv(c, map.hkv) * (int)map.hkv.d) * group + (u - rank * group);
   } else {
-    const int stride = classes | 1;
-    const int j = (slot / group) * kXcds + x;  // group, rank-major
-    rank = j / stride;
-    c = j % stride;
-    if (c >= classes) return false;
-    h = (c % Hkv) * group + slot % group;
+    const int stride = (int)map.stride.d;
+    const int sg = fdiv(slot, map.group);
+    const int j = sg * kXcds + x;  // group, rank-major
+    rank = fdiv(j, map.stride);
+    c = j - rank * stride;
+    if (c >= map.classes) return false;
+    h = (c - fdiv(c, map.hkv) * (int)map.hkv.d) * group + (slot - sg * group);
   }
   if (rank >= n_qt) return false;
-  b = c / Hkv;
+  b = fdiv(c, map.hkv);
   return true;
 }
 
 template <typename E, int MODE>
-__global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdParams p, int n_qt_max) {
+__global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdParams p, int n_qt_max,
+                                                                    const ItemMap map) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
 
   const int tid = threadIdx.x;
@@ -120,14 +157,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   const int rg = wave % kPfRowGroups;
   const int ks = wave / kPfRowGroups;
   int b, h, rank;
-  if (!prefill_item(blockIdx.x, p.Hkv, p.B * p.Hkv, p.group, n_qt_max, b, h, rank)) return;
+  if (!prefill_item(blockIdx.x, map, n_qt_max, b, h, rank)) return;
   // Work-group constants are made visibly uniform, so that everything derived from them (the load
   // addresses and sizes issued between the MFMAs) is scalar arithmetic, not VALU work that
   // competes with the other wave's softmax.
   b = __builtin_amdgcn_readfirstlane(b);
   h = __builtin_amdgcn_readfirstlane(h);
   rank = __builtin_amdgcn_readfirstlane(rank);
-  const int hk = __builtin_amdgcn_readfirstlane(h / p.group);
+  const int hk = __builtin_amdgcn_readfirstlane(fdiv(h, map.group));
 
   int T_b, kv_len;
   int64_t q_off, o_off, l_off, k_off, v_off;
@@ -638,7 +675,7 @@ static hipError_t launch_prefill_t(const FwdParams& p, int max_seqlen_q, hipStre
   if (n_qt == 0 || p.B == 0) return hipSuccess;
   const int grid = prefill_grid_size(p.B * p.Hkv, p.group, n_qt);
   hipLaunchKernelGGL((fa2_prefill_kernel<E, MODE>), dim3(grid), dim3(kPfThreads), 0, stream, p,
-                     n_qt);
+                     n_qt, make_item_map(p.B * p.Hkv, p.group, p.Hkv));
   return hipGetLastError();
 }
 
