@@ -18,9 +18,13 @@ A "step" is one call of the hot path on one batch of synthetic input, inputs res
       end to end, the Qwen2.5-1.5B architecture (random bf16 weights) serving 16 concurrent chats
       (prompts U[32, 1000], 64 tokens each) through the scheduler -> generated tok/s.
 
-Timing: W untimed warmup steps, then torch.cuda.synchronize(); a HIP event pair on the stream the
-kernels are launched on brackets exactly K steps; synchronize.  The per-launch duration is the
-event time / K.  The CPU baseline is the fp32 SDPA oracle (the reference's fallback path) on the
+Timing: each GPU workload first runs untimed for --ramp-ms (default 100 ms of wall time), which
+brings the GPU from its idle clock state to the clock it sustains under the load (the 4096 prefill:
+67-73 us per call over the first ~10 ms of calls from idle, a steady 60.0 us after 30 ms); then W
+untimed warmup steps, then torch.cuda.synchronize(); a HIP event pair on the stream the kernels are
+launched on brackets exactly K steps; synchronize.  The per-launch duration is the event time / K.
+The headline also reports `cold_clock`: the same W + K steps timed right after the input upload,
+before the ramp.  The CPU baseline is the fp32 SDPA oracle (the reference's fallback path) on the
 same inputs, on this host's cores (median of 5-21 runs per workload).
 
 --only runs one workload alone (for counter profiles: one kernel family per process); `copy` is a
@@ -30,6 +34,7 @@ counters.
 One GPU only: --gpus N > 1 exits with a message.
 """
 import argparse
+import gc
 import json
 import math
 import os
@@ -49,30 +54,68 @@ PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 flop/clk/CU
 PEAK_HBM_GBS = 8000.0      # HBM3E
 
 
-def _time_gpu(fn, steps, warmup):
-    """Average ms per call of fn() over exactly `steps` calls, HIP events on the current stream."""
+RAMP_MS = 100.0  # set from --ramp-ms in main()
+
+
+def _ramp(fn, ms):
+    """Runs fn() untimed for at least `ms` milliseconds of wall time (batches of 10 calls, each
+    batch synchronised), so that the GPU reaches the clock it sustains under this load: from idle
+    the 1 x 12 x 4096 causal prefill takes 67-73 us per call for the first ~10 ms of calls and a
+    steady 60.0 us after 30 ms or more."""
     import torch
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps):
-        fn(i)
-    end.record()
-    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        n += 10
+    return n
+
+
+def _time_gpu(fn, steps, warmup, ramp_ms=None):
+    """Average ms per call of fn() over exactly `steps` calls, HIP events on the current stream,
+    after the sustained-clock ramp (`_ramp`) and `warmup` untimed calls.
+
+    Python's garbage collector is run first and disabled from the ramp to the end of the timed
+    calls (as timeit does): the host enqueues a call in 35-50 us against a 50-70 us kernel, so a
+    collector pass of tens of milliseconds in the timed window -- the ramp's thousands of calls
+    make one likely -- would leave the GPU idle inside it (seen: 0.7-1.05 ms per call instead of
+    0.061), and one between the ramp and the timed calls would let the clock fall back."""
+    import torch
+    gc.collect()
+    enabled = gc.isenabled()
+    gc.disable()
+    try:
+        _ramp(fn, RAMP_MS if ramp_ms is None else ramp_ms)
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(steps):
+            fn(i)
+        end.record()
+        torch.cuda.synchronize()
+    finally:
+        if enabled:
+            gc.enable()
     return start.elapsed_time(end) / steps
 
 
-def bench_prefill(steps, warmup, seq_len=4096):
+def bench_prefill(steps, warmup, seq_len=4096, cold=False):
+    """With cold=True also returns the time of the same steps right after the input upload, before
+    the sustained-clock ramp (the GPU's idle clock state)."""
     import torch
     import workloads as wl
     from kernels.fa2 import FlashAttention2Function
     q, k, v = (t.cuda() for t in wl.prefill_single(seq_len, seed=0))
-    ms = _time_gpu(lambda i=0: FlashAttention2Function.apply(q, k, v, True, None), steps, warmup)
+    fn = lambda i=0: FlashAttention2Function.apply(q, k, v, True, None)
+    cold_ms = _time_gpu(fn, steps, warmup, ramp_ms=0.0) if cold else None
+    ms = _time_gpu(fn, steps, warmup)
     flops = wl.causal_prefill_flops([seq_len])
-    return ms, flops
+    return (ms, flops, cold_ms) if cold else (ms, flops)
 
 
 def bench_ragged(steps, warmup):
@@ -326,7 +369,12 @@ def main():
     ap.add_argument("--only", choices=("prefill", "decode", "ragged", "paged", "plumbing", "copy",
                                        "e2e"),
                     help="run one workload alone (counter profiles)")
+    ap.add_argument("--ramp-ms", type=float, default=100.0,
+                    help="untimed run of each GPU workload before its warmup, so that the GPU "
+                         "reaches its sustained clock (0: none)")
     args = ap.parse_args()
+    global RAMP_MS
+    RAMP_MS = args.ramp_ms
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's hot path runs on a single MI355X "
               f"(--gpus {args.gpus} is not supported)", file=sys.stderr)
@@ -338,7 +386,7 @@ def main():
         run_only(args.only, args.steps, args.warmup)
         return
 
-    ms, flops = bench_prefill(args.steps, args.warmup)
+    ms, flops, cold_ms = bench_prefill(args.steps, args.warmup, cold=True)
     tflops = flops / (ms * 1e-3) / 1e12
     out = {
         "metric": METRIC,
@@ -356,6 +404,11 @@ def main():
         "config": {"workload": "causal prefill attention, 1 sequence x 12 q heads / 2 kv heads x "
                                "4096 tokens x head_dim 128, bf16, N(0,1) seed 0",
                    "flops_per_step": flops},
+        "clock_ramp_ms": RAMP_MS,
+        "cold_clock": {"ms_per_step": round(cold_ms, 5),
+                       "value": round(flops / (cold_ms * 1e-3) / 1e12, 2),
+                       "note": "the same warmup + steps timed right after the input upload, before "
+                               "the untimed sustained-clock ramp that precedes every timed workload"},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": read_traffic("fa2_prefill_kernel")},
