@@ -305,31 +305,35 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   auto v0_start = [&](int j) { return j * kPfStep; };
   auto v1_start = [&](int j) { return (j - 1) * kPfStep + kPfBc; };
 
-  // Paged modes: the block-table entries of this wave's 8-row pairs of the 4 tiles of stage j,
-  // one per lane (lane t: tile t = K0, K1, V0, V1; -1 where nothing is loaded).  A table read is
-  // a vector load, and a wait for it would also wait for every LDS load in flight (the compiler
-  // cannot count those), so each stage's entries are fetched during the step before the one that
-  // issues its loads and arrive with that step's own loads.
-  auto tbl_fetch = [&](int j) -> int {
+  // Paged modes work on groups of 16 stages: group m is stages 16m - 1 .. 16m + 14, and lane l
+  // of a group register holds stage 16m - 1 + l/4, tile l%4 (K0, K1, V0, V1), so the table reads
+  // and address arithmetic of 16 steps cost the vector instructions of one.
+  //
+  // tbl_fetch(m): the block-table entries of this wave's 8-row pairs of group m's tiles (-1 where
+  // nothing is loaded).  A table read is a vector load, and a wait for it would also wait for
+  // every LDS load in flight (the compiler cannot count those), so a group's entries are fetched
+  // a whole group ahead and arrive with the loads of the step that fetches them.
+  auto tbl_fetch = [&](int m) -> int {
     if constexpr (is_paged(MODE)) {
+      const int j = 16 * m - 1 + (lane >> 2);
       const int t = lane & 3;
       const int ts = t == 0 ? k0_start(j) : t == 1 ? k1_start(j) : t == 2 ? v0_start(j) : v1_start(j);
       const int r0 = ts + 8 * wave;
-      if (lane < 4 && ts >= 0 && ts < kv_hi && r0 < kv_hi)
+      if (ts >= 0 && ts < kv_hi && r0 < kv_hi)
         return p.block_table[(int64_t)b * p.bt_stride + (r0 >> __builtin_ctz(p.block_size))];
       return -1;
     } else {
       return 0;
     }
   };
-  // Paged modes: the address and byte length of those pairs, lane t computing its own (the same
-  // lane layout): resolved from the entries once they have arrived -- at the start of the step
-  // that issues the loads, after the previous step's wait -- in a few vector instructions for
-  // all 4 at once.  A tile outside [0, kv_hi), an entry outside the pool or rows past kv_hi give
-  // a zero-length load.
-  auto resolve = [&](int j, int entry) -> PagedLoads {
+  // resolve(m, entries): the address and byte length of those pairs, each lane its own (the same
+  // lane layout), computed once the entries have arrived -- at the start of the step that issues
+  // the group's first loads -- in a few vector instructions for all 64.  A tile outside
+  // [0, kv_hi), an entry outside the pool or rows past kv_hi give a zero-length load.
+  auto resolve = [&](int m, int entry) -> PagedLoads {
     PagedLoads r{};
     if constexpr (is_paged(MODE)) {
+      const int j = 16 * m - 1 + (lane >> 2);
       const int t = lane & 3;
       const int ts = t == 0 ? k0_start(j) : t == 1 ? k1_start(j) : t == 2 ? v0_start(j) : v1_start(j);
       const int r0 = ts + 8 * wave;
@@ -350,18 +354,19 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
 
   // The 8 load instructions of a wave for stage j (which goes to LDS slot j & 1): 4 for K tiles,
   // 4 for V tiles, q = 2*tile + h.  Inside the key loop they are issued one at a time between the
-  // MFMAs of the score and PV phases rather than as a burst.  `tbl` holds stage j's table entries.
+  // MFMAs of the score and PV phases rather than as a burst.  Paged modes: `pl` is the resolved
+  // group holding stage j, whose tiles sit in lanes 4 * ((j + 1) % 16) + tile.
   auto dma_k = [&](int j, int q, const PagedLoads& pl) {
     const int o = (j & 1) * kStageBytes + (q >> 1) * kTileBytes;  // j & 1 folds when j's parity is known
-    dma_one(p.k, k_off, p.k_st, (q >> 1) ? k1_start(j) : k0_start(j), o, k_voff, q & 1, pl, q >> 1);
+    dma_one(p.k, k_off, p.k_st, (q >> 1) ? k1_start(j) : k0_start(j), o, k_voff, q & 1, pl,
+            4 * ((j + 1) & 15) + (q >> 1));
   };
   auto dma_v = [&](int j, int q, const PagedLoads& pl) {
     const int o = kVRegion + (j & 1) * kStageBytes + (q >> 1) * kTileBytes;
     dma_one(p.v, v_off, p.v_st, (q >> 1) ? v1_start(j) : v0_start(j), o, v_voff, q & 1, pl,
-            2 + (q >> 1));
+            4 * ((j + 1) & 15) + 2 + (q >> 1));
   };
-  auto load_stage = [&](int j) {
-    const PagedLoads pl = resolve(j, tbl_fetch(j));
+  auto load_stage = [&](int j, const PagedLoads& pl) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) dma_k(j, q, pl);
 #pragma unroll
@@ -520,11 +525,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   };
 
   // Prologue: stage -1 (slot 1) holds K(0,0) for stream 0's first scores, stage 0 goes to slot 0.
-  int tbl[2] = {0, 0};  // tbl[j & 1]: table entries of stage j + 1, whose loads step j issues
+  // Paged modes: pl holds the loads of the current group of 16 stages, tbl the table entries of
+  // the next group.
+  PagedLoads pl{};
+  int tbl = 0;
   if (n_steps > 0) {
-    load_stage(-1);
-    load_stage(0);
-    tbl[0] = tbl_fetch(1);
+    pl = resolve(0, tbl_fetch(0));
+    load_stage(-1, pl);
+    load_stage(0, pl);
+    tbl = tbl_fetch(1);
   }
   // Every path reaches the loop with no vector load in flight (the Q registers included).
   stage_ready();
@@ -539,7 +548,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     // the step into an immediate (the loop below is unrolled by two for that).
     auto step = [&](int j, auto par) {
       constexpr int slot = decltype(par)::value;
-      const PagedLoads pl = resolve(2 * (j >> 1) + slot + 1, tbl[slot]);
+      // Stage j + 1, which this step loads, starts a group when j + 2 is a multiple of 16.
+      if (is_paged(MODE) && slot == 0 && ((j + 2) & 15) == 0) {
+        pl = resolve((j + 2) >> 4, tbl);
+        tbl = tbl_fetch(((j + 2) >> 4) + 1);
+      }
       auto next_v = [&](int q) { dma_v(2 * (j >> 1) + slot + 1, q, pl); };
       auto next_k = [&](int q) { dma_k(2 * (j >> 1) + slot + 1, q, pl); };
       if (active(j)) {
@@ -556,7 +569,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
 #pragma unroll
         for (int q = 0; q < 4; ++q) next_k(q);
       }
-      tbl[slot ^ 1] = tbl_fetch(2 * (j >> 1) + slot + 2);
       stage_ready();
     };
     int j = 0;
@@ -571,7 +583,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     __syncthreads();
     auto step = [&](int j, auto par) {
       constexpr int slot = decltype(par)::value;
-      const PagedLoads pl = resolve(2 * (j >> 1) + slot + 1, tbl[slot]);
+      // Stage j + 1, which this step loads, starts a group when j + 2 is a multiple of 16.
+      if (is_paged(MODE) && slot == 0 && ((j + 2) & 15) == 0) {
+        pl = resolve((j + 2) >> 4, tbl);
+        tbl = tbl_fetch(((j + 2) >> 4) + 1);
+      }
       auto next_v = [&](int q) { dma_v(2 * (j >> 1) + slot + 1, q, pl); };
       auto next_k = [&](int q) { dma_k(2 * (j >> 1) + slot + 1, q, pl); };
       if (active(j - 1)) {
@@ -588,7 +604,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
 #pragma unroll
         for (int q = 0; q < 4; ++q) next_k(q);
       }
-      tbl[slot ^ 1] = tbl_fetch(2 * (j >> 1) + slot + 2);
       stage_ready();
     };
     int j = 0;
