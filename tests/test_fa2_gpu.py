@@ -329,6 +329,35 @@ def test_paged_block_size_32():
     check_close(out, _paged_ref(q, kp, vp, tables, lens, bs, False), what="bs32")
 
 
+@pytest.mark.parametrize("bs", [16, 32])
+def test_paged_prefill_rows_across_table_groups_equal_dense(bs):
+    # The paged prefill resolves block-table entries 16 steps (of 128 keys) at a time; rows whose
+    # key walks end just before, at and after those group boundaries (15-17 and 32 steps), causal
+    # and not, must give the dense kernel's bits on the gathered K/V, and the oracle's values.
+    g = torch.Generator().manual_seed(21)
+    lens = [1919, 1920, 1921, 2047, 2048, 2049, 2177, 4095]
+    T = 65
+    num_blocks = sum(math.ceil(n / bs) for n in lens) + 8
+    tables = opaged.random_tables(lens, bs, num_blocks, g)
+    kp = torch.randn(num_blocks * bs, 2, 128, generator=g).to(torch.bfloat16)
+    vp = torch.randn(num_blocks * bs, 2, 128, generator=g).to(torch.bfloat16)
+    q = torch.randn(len(lens), 12, T, 128, generator=g).to(torch.bfloat16)
+    S = max(lens)
+    kd = opaged.gather_dense(kp, tables, S, bs).contiguous()
+    vd = opaged.gather_dense(vp, tables, S, bs).contiguous()
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    bt = wl.table_tensor(tables).to(DEV)
+    for causal in (True, False):
+        announce(f"[gpu] paged prefill across table groups, block_size {bs}, causal {causal}")
+        o_dense = FlashAttention2Function.apply(q.to(DEV), kd.to(DEV), vd.to(DEV), causal, lens_t)
+        o_paged = fa2_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), bt, lens_t, max_kv_len=S,
+                            is_causal=causal, block_size=bs)
+        torch.cuda.synchronize()
+        assert torch.equal(o_dense.cpu(), o_paged.cpu())
+        check_close(o_paged, _paged_ref(q, kp, vp, tables, lens, bs, causal),
+                    what=f"paged prefill across groups bs{bs} causal{causal}")
+
+
 def test_empty_rows_and_queries_without_keys_give_zero():
     g = torch.Generator().manual_seed(7)
     q = torch.randn(3, 12, 20, 128, generator=g).to(torch.bfloat16)
