@@ -75,6 +75,9 @@ struct Parity {
 //     different lengths spread over all XCDs instead of pinning a class -- and its row's whole
 //     work -- to XCD c % 8 (16 ragged rows of U[16, 1024] tokens: the busiest XCD carried 1.9x
 //     the least busy one's tiles that way).
+//   * packed batches of at most 64 rows (the varlen modes) number only the real (class, rank)
+//     groups, rank-major, and deal group j to XCD j % 8 (prefill_item_packed): a row's class moves
+//     over the XCDs as shorter rows drop out of the later ranks.
 constexpr int kXcds = 8;
 
 __host__ __device__ inline int prefill_grid_size(int classes, int group, int n_qt) {
@@ -146,6 +149,44 @@ __device__ inline bool prefill_item(int w, const ItemMap& map, int n_qt, int& b,
   return true;
 }
 
+// Packed batches of at most 64 rows (the varlen modes).  The grid is sized for every row having the
+// longest row's tile count; prefill_item leaves the ranks past a short row's last tile as padding
+// work-groups between the real ones, and each held a CU for about a microsecond (840 of the 1,584
+// work-groups of 16 rows of U[16, 1024] tokens).  Here the groups (rank, class) are numbered over
+// the real tiles only, rank-major and in row order within a rank, so all padding falls at the end
+// of the grid, where it delays nothing.  Every wave finds its item from the rows' query counts (one
+// load per lane, a ballot per rank), so no barrier is needed.
+__device__ inline bool prefill_item_packed(const FwdParams& p, int w, const ItemMap& map,
+                                           int n_qt, int& b, int& h, int& rank) {
+  const int lane = threadIdx.x & 63;
+  int nq = 0;
+  if (lane < p.B) {
+    const int t = p.cu_q[lane + 1] - p.cu_q[lane];
+    nq = t > 0 ? (t + kPfRows - 1) / kPfRows : 0;
+  }
+  const int x = w % kXcds, slot = w / kXcds;
+  const int sg = fdiv(slot, map.group);
+  const int hkv = (int)map.hkv.d;
+  int j = sg * kXcds + x;  // the j-th real group (rank, class), rank-major
+  int r = 0;
+  uint64_t rows = 0;
+  for (; r < n_qt; ++r) {
+    rows = __ballot(nq > r);
+    const int cnt = __builtin_amdgcn_readfirstlane(__popcll(rows) * hkv);
+    if (j < cnt) break;
+    j -= cnt;
+  }
+  // Row b is the ri-th row (lowest first) that has a tile of rank r.
+  const int ri = fdiv(j, map.hkv);
+  const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(rows >> 32),
+                                               __builtin_amdgcn_mbcnt_lo((uint32_t)rows, 0));
+  b = __builtin_amdgcn_readfirstlane(
+      __builtin_ctzll(__ballot(nq > r && below == ri) | (1ull << 63)));
+  h = (j - ri * hkv) * (int)map.group.d + (slot - sg * (int)map.group.d);
+  rank = r;
+  return r < n_qt;
+}
+
 template <typename E, int MODE>
 __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdParams p, int n_qt_max,
                                                                     const ItemMap map) {
@@ -157,7 +198,13 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   const int rg = wave % kPfRowGroups;
   const int ks = wave / kPfRowGroups;
   int b, h, rank;
-  if (!prefill_item(blockIdx.x, map, n_qt_max, b, h, rank)) return;
+  bool real;
+  if constexpr (MODE == kVarlen || MODE == kPagedVarlen)
+    real = p.B <= 64 ? prefill_item_packed(p, blockIdx.x, map, n_qt_max, b, h, rank)
+                     : prefill_item(blockIdx.x, map, n_qt_max, b, h, rank);
+  else
+    real = prefill_item(blockIdx.x, map, n_qt_max, b, h, rank);
+  if (!real) return;
   // Work-group constants are made visibly uniform, so that everything derived from them (the load
   // addresses and sizes issued between the MFMAs) is scalar arithmetic, not VALU work that
   // competes with the other wave's softmax.
@@ -688,7 +735,11 @@ template <typename E, int MODE>
 static hipError_t launch_prefill_t(const FwdParams& p, int max_seqlen_q, hipStream_t stream) {
   const int n_qt = (max_seqlen_q + kPfRows - 1) / kPfRows;
   if (n_qt == 0 || p.B == 0) return hipSuccess;
-  const int grid = prefill_grid_size(p.B * p.Hkv, p.group, n_qt);
+  // Packed batches: one slot per (rank, class, query head) of the full B x n_qt box, numbered by
+  // prefill_item_packed (real tiles first).
+  const bool packed = (MODE == kVarlen || MODE == kPagedVarlen) && p.B <= 64;
+  const int grid = packed ? kXcds * p.group * ((p.B * p.Hkv * n_qt + kXcds - 1) / kXcds)
+                          : prefill_grid_size(p.B * p.Hkv, p.group, n_qt);
   hipLaunchKernelGGL((fa2_prefill_kernel<E, MODE>), dim3(grid), dim3(kPfThreads), 0, stream, p,
                      n_qt, make_item_map(p.B * p.Hkv, p.group, p.Hkv));
   return hipGetLastError();
