@@ -141,12 +141,16 @@ def test_ragged_varlen_prefill():
 def test_varlen_every_tile_is_written_for_any_row_count(causal):
     """Rows x kv heads (the work-group classes) of every count, dividing 8 or not, ragged lengths
     from 1 to 700 (empty rows too): each output row is written exactly as the oracle's.  The
-    output starts as NaN, so a tile the grid misses fails the finite check."""
+    output starts as NaN, so a tile the grid misses fails the finite check.  64 rows is the
+    largest batch whose tiles are numbered over the real tiles only; 65 takes the plain mapping."""
     g = torch.Generator().manual_seed(21)
-    for B in (1, 3, 4, 5, 7, 9, 13, 21):
-        lens = torch.randint(1, 701, (B,), generator=g).tolist()
+    for B in (1, 3, 4, 5, 7, 9, 13, 21, 64, 65):
+        lens = torch.randint(1, 701 if B < 64 else 301, (B,), generator=g).tolist()
         if B > 3:
             lens[2] = 0
+        if B >= 64:
+            lens[40] = 0
+            lens[63] = 700
         cu = [0]
         for n in lens:
             cu.append(cu[-1] + n)
@@ -159,7 +163,12 @@ def test_varlen_every_tile_is_written_for_any_row_count(causal):
         fa2_varlen(q.to(DEV), k.to(DEV), v.to(DEV), cu_t, cu_t, max(lens), is_causal=causal,
                    out=out)
         torch.cuda.synchronize()
-        check_close(out, sdpa.varlen_ref(q, k, v, cu, cu, causal), what=f"B={B}")
+        # The 64- and 65-row batches hold 20k+ query rows, many of them short (a few keys, peaked
+        # softmax), and their largest error is the bf16 rounding of P and of an output above 2
+        # (half an ulp there is 7.8e-3): measured 1.08e-2 at 65 rows, so they use the reference
+        # test's own bar, 2e-2 (kernels/test_fa2.py:25); the mean-abs bar stays 1e-3.
+        check_close(out, sdpa.varlen_ref(q, k, v, cu, cu, causal),
+                    max_abs=MAX_ABS if B < 64 else 2e-2, what=f"B={B}")
 
 
 def test_varlen_with_longer_keys_than_queries():
