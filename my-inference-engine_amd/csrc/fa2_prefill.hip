@@ -31,8 +31,9 @@
 //     deliver.  The swizzles make every LDS read of the loop bank-conflict free.
 //   * Each load instruction moves 4 key rows (1 KB) through a buffer resource that starts at the
 //     first of them and ends at the last key the work-group needs: keys past it read as zeros,
-//     with no per-lane predicate.  In paged mode the 4 rows always share one block, so the block
-//     table is read once per instruction, by the scalar unit.
+//     with no per-lane predicate.  In paged mode a wave's two instructions of a tile (8 rows)
+//     share one block; the block-table entries of 16 steps are fetched with one vector load and
+//     turned into load addresses in one vector pass, each instruction reading its own back.
 //   * LDS holds two stages of (K, V) for both streams; the next 128 keys are loaded while the
 //     current ones are computed, one barrier per 128 keys.
 //   * Masking runs only on tiles that straddle the causal diagonal or the end of the row, and tiles
@@ -414,10 +415,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
             4 * ((j + 1) & 15) + 2 + (q >> 1));
   };
   auto load_stage = [&](int j, const PagedLoads& pl) {
+    // Prologue stages only (j = -1, 0, constants): a tile that starts before key 0 holds nothing
+    // any wave reads (stage -1: K1, V0 and V1; stage 0: V1), so its loads are not issued.  Each
+    // load instruction costs its wave about 34 issue cycles and 1 KB of LDS writes even when it
+    // only writes zeros.
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dma_k(j, q, pl);
+    for (int q = 0; q < 4; ++q)
+      if (((q >> 1) ? k1_start(j) : k0_start(j)) >= 0) dma_k(j, q, pl);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dma_v(j, q, pl);
+    for (int q = 0; q < 4; ++q)
+      if (((q >> 1) ? v1_start(j) : v0_start(j)) >= 0) dma_v(j, q, pl);
   };
   // Each wave waits for its own loads, then the barrier publishes them to the work-group.
   // The builtin wait tells the compiler its own loads (Q) are done; the assembly one is the real
