@@ -671,69 +671,94 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     __syncthreads();
   }
 
-  // Merge stream 1 into stream 0 through LDS: [row group][64 O values + m + l][lane].
+  // The two streams of a row group split the epilogue: each gives the other the half of O it does
+  // not keep (stream 0 keeps d 0..63, stream 1 d 64..127) with its (m, l), merges its own half
+  // and stores it, so the merge, the normalisation and the stores run on all 8 waves instead of
+  // stream 0's 4 (16 packed sequences 43.2 -> 40.5 us, 768 equal 1024-key tiles 66.6 -> 64.9 us).
+  // Exchange area of wave (rg, ks): [32 O values + m + l][lane].
   float* red = reinterpret_cast<float*>(smem);
-  constexpr int kRedVals = 66;
-  if (ks == 1) {
-    float* dst = red + rg * kRedVals * 64 + lane;
+  constexpr int kXVals = 34;
+  {
+    float* dst = red + (rg * kPfStreams + ks) * kXVals * 64 + lane;
+    // d-blocks handed over (whole-vector selects on the wave-uniform stream: a runtime index
+    // into the accumulators would put them in scratch memory)
+    const f32x16 give0 = ks == 0 ? oacc[2] : oacc[0];
+    const f32x16 give1 = ks == 0 ? oacc[3] : oacc[1];
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) dst[(db * 16 + r) * 64] = oacc[db][r];
-    dst[64 * 64] = m_run;
-    dst[65 * 64] = l_run;
+    for (int r = 0; r < 16; ++r) {
+      dst[r * 64] = give0[r];
+      dst[(16 + r) * 64] = give1[r];
+    }
+    dst[32 * 64] = m_run;
+    dst[33 * 64] = l_run;
   }
   __syncthreads();
-  if (ks == 1) return;
-  // Rows past T_b keep their lanes for the row-wise stores below (their values are merged,
-  // harmlessly, and never stored).
+  const int keep = ks == 0 ? 0 : 2;  // first d-block kept
+  const f32x16 keep0 = ks == 0 ? oacc[0] : oacc[2];
+  const f32x16 keep1 = ks == 0 ? oacc[1] : oacc[3];
+  f32x16 ok[2];
   {
-    const float* src = red + rg * kRedVals * 64 + lane;
-    const float m1 = src[64 * 64];
-    const float l1 = src[65 * 64];
-    const float M = fmaxf(m_run, m1);
+    // Rows past T_b keep their lanes for the row-wise stores below (their values are merged,
+    // harmlessly, and never stored).
+    const float* src = red + (rg * kPfStreams + (ks ^ 1)) * kXVals * 64 + lane;
+    // Both streams evaluate the same expression, O = O_0 f_0 + O_1 f_1 with stream 0's state
+    // first, so each half of a row is rounded as if one wave merged the whole row.
+    const float mo = src[32 * 64];
+    const float lo = src[33 * 64];
+    const float M = ks == 0 ? fmaxf(m_run, mo) : fmaxf(mo, m_run);
     const float M_use = M == -INFINITY ? 0.f : M;
-    const float f0 = exp2_fast(m_run - M_use);
-    const float f1 = exp2_fast(m1 - M_use);
+    const float fs = exp2_fast(m_run - M_use);  // this stream's factor
+    const float fo = exp2_fast(mo - M_use);     // the other's
+    // fma(O_0, f_0, O_1 f_1) spelled out, so that the compiler cannot contract the two streams'
+    // expressions differently.
+    if (ks == 0) {
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+      for (int r = 0; r < 16; ++r) {
+        ok[0][r] = __builtin_fmaf(keep0[r], fs, src[r * 64] * fo);
+        ok[1][r] = __builtin_fmaf(keep1[r], fs, src[(16 + r) * 64] * fo);
+      }
+      l_run = __builtin_fmaf(l_run, fs, lo * fo);
+    } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[db][r] = oacc[db][r] * f0 + src[(db * 16 + r) * 64] * f1;
-    l_run = l_run * f0 + l1 * f1;
+      for (int r = 0; r < 16; ++r) {
+        ok[0][r] = __builtin_fmaf(src[r * 64], fo, keep0[r] * fs);
+        ok[1][r] = __builtin_fmaf(src[(16 + r) * 64], fo, keep1[r] * fs);
+      }
+      l_run = __builtin_fmaf(lo, fo, l_run * fs);
+    }
     m_run = M;
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   // Accumulator r of d-block db is d = 32*db + 8*(r/4) + 4*g + r%4: four consecutive d per group.
-  // The wave's O rows go through LDS so that every global store writes whole rows: row-major
-  // [32 rows][128 d] in this row group's part of the merge area (already read above; LDS
-  // operations of one wave run in order), 16-byte chunks XOR-swizzled by row % 16 so that the
-  // writes (32 rows, one chunk each) and the reads (16 chunks of a row) spread over all banks.
-  // Direct stores from the MFMA layout write 16 bytes into each of 32 rows per instruction: 7%
-  // slower on 16 packed sequences, 5% slower on 768 equal 1024-key tiles, the same on one
-  // 4096-token sequence.
+  // The wave's half rows go through LDS so that every global store writes whole 128-byte
+  // half rows: row-major [32 rows][64 d] in this wave's staging area (after the exchange areas),
+  // 16-byte chunks XOR-swizzled by row % 8 so that the writes and the reads spread over the banks.
+  // Direct stores from the MFMA layout (16 bytes into each of 32 rows per instruction) measured
+  // 5-7% slower on short tiles when one wave stored whole rows.
   {
-    uint8_t* ot = reinterpret_cast<uint8_t*>(red + rg * kRedVals * 64);
+    uint8_t* ot = reinterpret_cast<uint8_t*>(red + kPfWaves * kXVals * 64) + wave * (32 * 128);
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+    for (int i = 0; i < 2; ++i) {
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const u32x2 val = {E::pack2(oacc[db][rr * 4] * inv, oacc[db][rr * 4 + 1] * inv),
-                           E::pack2(oacc[db][rr * 4 + 2] * inv, oacc[db][rr * 4 + 3] * inv)};
-        *reinterpret_cast<u32x2*>(ot + r32 * 256 + 16 * ((4 * db + rr) ^ (r32 & 15)) + 8 * g) = val;
+        const u32x2 val = {E::pack2(ok[i][rr * 4] * inv, ok[i][rr * 4 + 1] * inv),
+                           E::pack2(ok[i][rr * 4 + 2] * inv, ok[i][rr * 4 + 3] * inv)};
+        *reinterpret_cast<u32x2*>(ot + r32 * 128 + 16 * ((4 * i + rr) ^ (r32 & 7)) + 8 * g) = val;
       }
     }
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {  // rows 4k .. 4k+3, one 16-byte chunk per lane
-      const int row = 4 * k + (lane >> 4), ch = lane & 15;
-      const u32x4 val = *reinterpret_cast<const u32x4*>(ot + row * 256 + 16 * (ch ^ (row & 15)));
+    for (int k = 0; k < 4; ++k) {  // rows 8k .. 8k+7, one 16-byte chunk per lane
+      const int row = 8 * k + (lane >> 3), ch = lane & 7;
+      const u32x4 val = *reinterpret_cast<const u32x4*>(ot + row * 128 + 16 * (ch ^ (row & 7)));
       if (wq0 + row < T_b)
-        *reinterpret_cast<u32x4*>(p.o + o_off + (int64_t)(wq0 + row) * p.o_st + ch * 8) = val;
+        *reinterpret_cast<u32x4*>(p.o + o_off + (int64_t)(wq0 + row) * p.o_st + keep * 32 +
+                                  ch * 8) = val;
     }
   }
-  if (p.lse && g == 0 && qrow < T_b)
+  if (ks == 0 && p.lse && g == 0 && qrow < T_b)
     p.lse[l_off + (int64_t)qrow * p.l_st] =
         l_tot > 0.f ? (m_run + __builtin_log2f(l_tot)) * kLn2 : -INFINITY;
 }
