@@ -14,10 +14,11 @@
  *   - Strides are in ELEMENTS, int64.  The innermost (head_dim) stride must be 1, every other stride
  *     a multiple of 8 elements and every tensor base 16-byte aligned (16-byte vector loads).
  *   - `dtype` is MI_FA2_BF16 or MI_FA2_FP16; q, k, v and o share it (the sampler also takes
- *     MI_FA2_FP32 logits).  Softmax and accumulation
+ *     MI_FA2_FP32 logits, mi_fa2_fwd_general MI_FA2_FP32 inputs).  Softmax and accumulation
  *     are fp32; `lse` is fp32 (natural log, like the reference's L, kernels/fa2.py:158,189).
- *   - head_dim must be 128 (the Qwen2.5 shape); heads_q must be a multiple of heads_kv and query
- *     head h reads kv head h / (heads_q / heads_kv) (kernels/fa2.py:53, model.py:70-75).
+ *   - head_dim must be 128 (the Qwen2.5 shape) except in mi_fa2_fwd_general; heads_q must be a
+ *     multiple of heads_kv and query head h reads kv head h / (heads_q / heads_kv)
+ *     (kernels/fa2.py:53, model.py:70-75).
  *   - Causal masking is bottom-right aligned per row: query i of a row sees key j iff
  *     j <= i + kv_len - seqlen_q (kernels/fa2.py:109-111,132-138).  Keys j >= kv_len are never read
  *     as data: their loads are predicated off, so padding may hold anything, NaN included.
@@ -78,6 +79,27 @@ MI_FA2_API int mi_fa2_fwd(int32_t dtype, const void* q, const void* k, const voi
                const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
                const int64_t* o_strides, const int64_t* lse_strides, int32_t is_causal,
                float sm_scale, void* workspace, size_t workspace_bytes, mi_fa2_stream_t stream);
+
+/*
+ * Padded forward over the rest of the launcher's envelope.  Replaces FlashAttention2Function.forward
+ * (kernels/fa2.py:164-214) for the inputs mi_fa2_fwd does not take: head dims that are any powers of
+ * two from 16 to 256 (kernels/fa2.py:185), with d_v (V and O) allowed to differ from d (Q and K),
+ * and fp32 inputs, whose dots stay fp32 (input_precision="ieee", kernels/fa2.py:129,147).
+ *   dtype: MI_FA2_BF16, MI_FA2_FP16 or MI_FA2_FP32 (q, k, v and o share it);
+ *   q [batch, heads_q, seqlen_q, head_dim], k [batch, heads_kv, seqlen_k, head_dim],
+ *   v [batch, heads_kv, seqlen_k, head_dim_v], o [batch, heads_q, seqlen_q, head_dim_v];
+ *   everything else as in mi_fa2_fwd (kv_lens clamped to [0, seqlen_k], bottom-right causal mask,
+ *   lse may be NULL).  batch and heads_q are at most 65535.  One kernel (16x16 MFMAs, no LDS, no
+ *   workspace) serves every seqlen_q; bf16/fp16 at head_dim = head_dim_v = 128 is faster through
+ *   mi_fa2_fwd, which this entry point does not dispatch to.
+ */
+MI_FA2_API int mi_fa2_fwd_general(int32_t dtype, const void* q, const void* k, const void* v, void* o,
+                       float* lse, const int32_t* kv_lens, int32_t batch, int32_t heads_q,
+                       int32_t heads_kv, int32_t seqlen_q, int32_t seqlen_k, int32_t head_dim,
+                       int32_t head_dim_v, const int64_t* q_strides, const int64_t* k_strides,
+                       const int64_t* v_strides, const int64_t* o_strides,
+                       const int64_t* lse_strides, int32_t is_causal, float sm_scale,
+                       mi_fa2_stream_t stream);
 
 /*
  * Packed variable-length forward.  The reference has no packed entry point: it pads a ragged

@@ -16,6 +16,7 @@ namespace mi_fa2 {
 hipError_t launch_prefill(const FwdParams& p, int dtype, int mode, int max_seqlen_q,
                           hipStream_t stream);
 hipError_t launch_decode(const FwdParams& p, int dtype, int mode, hipStream_t stream);
+hipError_t launch_general(const FwdParams& p, int dtype, int d, int dv, hipStream_t stream);
 hipError_t launch_merge(const MergeParams& p, int out_dtype, hipStream_t stream);
 hipError_t launch_rope_kv(const RopeParams& p, int dtype, hipStream_t stream);
 hipError_t launch_sample(const SampleParams& p, int dtype, hipStream_t stream);
@@ -330,6 +331,62 @@ int mi_fa2_fwd(int32_t dtype, const void* q, const void* k, const void* v, void*
     return launched(mi_fa2::launch_decode(p, dtype, mi_fa2::kDense, s));
   }
   return launched(mi_fa2::launch_prefill(p, dtype, mi_fa2::kDense, seqlen_q, s));
+}
+
+int mi_fa2_fwd_general(int32_t dtype, const void* q, const void* k, const void* v, void* o,
+                       float* lse, const int32_t* kv_lens, int32_t batch, int32_t heads_q,
+                       int32_t heads_kv, int32_t seqlen_q, int32_t seqlen_k, int32_t head_dim,
+                       int32_t head_dim_v, const int64_t* q_strides, const int64_t* k_strides,
+                       const int64_t* v_strides, const int64_t* o_strides,
+                       const int64_t* lse_strides, int32_t is_causal, float sm_scale,
+                       mi_fa2_stream_t stream) {
+  if (dtype != MI_FA2_BF16 && dtype != MI_FA2_FP16 && dtype != MI_FA2_FP32)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "dtype %d is not bf16 (0), fp16 (1) or fp32 (2)", dtype);
+  auto dim_ok = [](int32_t d) { return d == 16 || d == 32 || d == 64 || d == 128 || d == 256; };
+  if (!dim_ok(head_dim) || !dim_ok(head_dim_v))
+    return fail(MI_FA2_ERR_UNSUPPORTED,
+                "head_dim %d / head_dim_v %d: each must be a power of two from 16 to 256", head_dim,
+                head_dim_v);
+  if (batch < 0 || heads_q <= 0 || heads_kv <= 0 || heads_q % heads_kv != 0)
+    return fail(MI_FA2_ERR_INVALID, "bad sizes: batch=%d heads_q=%d heads_kv=%d", batch, heads_q,
+                heads_kv);
+  if (batch > 65535 || heads_q > 65535)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "batch (%d) and heads_q (%d) are at most 65535", batch,
+                heads_q);
+  if (seqlen_q < 0 || seqlen_k < 0)
+    return fail(MI_FA2_ERR_INVALID, "bad lengths: seqlen_q=%d seqlen_k=%d", seqlen_q, seqlen_k);
+  if (batch == 0 || seqlen_q == 0) return ok();
+  if (int rc = check_tensor("q", q, q_strides, 3)) return rc;
+  if (int rc = check_tensor("o", o, o_strides, 3)) return rc;
+  if (seqlen_k > 0) {
+    if (int rc = check_tensor("k", k, k_strides, 3)) return rc;
+    if (int rc = check_tensor("v", v, v_strides, 3)) return rc;
+  }
+  if (lse && !lse_strides) return fail(MI_FA2_ERR_INVALID, "lse strides are NULL");
+
+  FwdParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.o = static_cast<uint16_t*>(o);
+  p.kv_lens = kv_lens;
+  p.q_sb = q_strides[0], p.q_sh = q_strides[1], p.q_st = q_strides[2];
+  p.o_sb = o_strides[0], p.o_sh = o_strides[1], p.o_st = o_strides[2];
+  if (seqlen_k > 0) {
+    p.k_sb = k_strides[0], p.k_sh = k_strides[1], p.k_st = k_strides[2];
+    p.v_sb = v_strides[0], p.v_sh = v_strides[1], p.v_st = v_strides[2];
+  }
+  set_lse(p, lse, lse_strides, 3);
+  p.B = batch;
+  p.Hq = heads_q;
+  p.Hkv = heads_kv;
+  p.group = heads_q / heads_kv;
+  p.T = seqlen_q;
+  p.S = seqlen_k;
+  p.causal = is_causal ? 1 : 0;
+  p.scale_log2 = sm_scale * mi_fa2::kLog2e;
+  return launched(mi_fa2::launch_general(p, dtype, head_dim, head_dim_v,
+                                         reinterpret_cast<hipStream_t>(stream)));
 }
 
 int mi_fa2_fwd_varlen(int32_t dtype, const void* q, const void* k, const void* v, void* o,

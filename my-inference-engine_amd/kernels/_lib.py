@@ -16,6 +16,7 @@ LIB_PATH = Path(os.environ.get("MI_FA2_LIB", Path(__file__).resolve().parent / "
 
 OK = 0
 DTYPES = {torch.bfloat16: 0, torch.float16: 1}
+GENERAL_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}  # mi_fa2_fwd_general
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -30,6 +31,8 @@ SIGNATURES = {
     "mi_fa2_fwd_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "mi_fa2_fwd": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
                           _p, _p, _p, _p, _p, _i32, _f32, _p, _sz, _p]),
+    "mi_fa2_fwd_general": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32,
+                                  _i32, _i32, _p, _p, _p, _p, _p, _i32, _f32, _p]),
     "mi_fa2_fwd_varlen": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32,
                                  _p, _p, _p, _p, _p, _i32, _f32, _p]),
     "mi_fa2_fwd_paged_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),

@@ -7,7 +7,9 @@ reference's model.py:11-15,102-103 import and call it unchanged.  The Triton lau
 gfx950 kernels on torch's current stream:
 
   * seqlen_q > 1: the MFMA prefill kernel (csrc/fa2_prefill.hip);
-  * seqlen_q == 1: the split-KV decode kernel + combine (csrc/fa2_decode.hip).
+  * seqlen_q == 1: the split-KV decode kernel + combine (csrc/fa2_decode.hip);
+  * any other head dims (powers of two from 16 to 256, d_v may differ from d) or fp32 inputs: the
+    general kernel (csrc/fa2_general.hip), for every seqlen_q.
 
 Three entry points go beyond the reference's padded call:
 
@@ -20,8 +22,10 @@ Three entry points go beyond the reference's padded call:
     runs packed rows with different new-token counts over the paged pool in one launch (the
     prompts of a mixed prefill + decode step).
 
-The HIP kernels cover head_dim 128 in bf16/fp16 (the Qwen2.5-1.5B shape the engine runs).
-Anything else is rejected with an AssertionError, never silently computed another way.
+The paged and packed entry points cover head_dim 128 in bf16/fp16 (the Qwen2.5-1.5B shape the
+engine runs); the padded call also takes the rest of the reference's envelope (kernels/fa2.py:185:
+power-of-two d and d_v; fp32 inputs with fp32 dots, kernels/fa2.py:129,147) up to 256.  Anything
+else is rejected with an AssertionError, never silently computed another way.
 """
 import math
 
@@ -46,6 +50,20 @@ def _strides(t):
     # a size-1 dimension is only ever indexed at 0, so its stride is irrelevant: pass 0
     s = [0 if n == 1 else st for st, n in zip(t.stride(), t.shape)]
     return (_lib.ctypes.c_int64 * len(s))(*s)
+
+
+GENERAL_DIMS = (16, 32, 64, 128, 256)
+
+
+def _general_envelope(Q, K, V):
+    """The general kernel's envelope: bf16/fp16/fp32, power-of-two d and d_v from 16 to 256."""
+    assert Q.dtype in _lib.GENERAL_DTYPES, \
+        f"the MI355X kernels take bf16, fp16 or fp32 inputs, got {Q.dtype}"
+    assert K.dtype == Q.dtype and V.dtype == Q.dtype, "Q, K and V must share one dtype"
+    assert Q.shape[-1] in GENERAL_DIMS and V.shape[-1] in GENERAL_DIMS, (
+        f"the MI355X kernels take head dims 16 to 256, got d={Q.shape[-1]}, d_v={V.shape[-1]}")
+    assert K.device == Q.device and V.device == Q.device, "Q, K and V must be on one device"
+    assert Q.shape[0] <= 65535 and Q.shape[1] <= 65535, "batch and heads are at most 65535"
 
 
 def _envelope(Q, K, V):
@@ -105,12 +123,29 @@ class FlashAttention2Function(torch.autograd.Function):
                 "kv_lens must be an int32 tensor of shape [batch]"
             assert kv_lens.device == Q.device, "kv_lens must be on Q's device"
         assert (d & (d - 1) == 0) and (d_v & (d_v - 1) == 0), "d and d_v must be powers of 2"
-        _envelope(Q, K, V)
+        fast = Q.dtype in _lib.DTYPES and d == HEAD_DIM and d_v == HEAD_DIM
+        if fast:
+            _envelope(Q, K, V)
+        else:
+            _general_envelope(Q, K, V)
 
         O = torch.empty((batch_size, num_heads, seq_len, d_v), device=Q.device, dtype=Q.dtype)
         L = torch.empty((batch_size, num_heads, seq_len), device=Q.device, dtype=torch.float32)
         q, k, v = _vec(Q), _vec(K), _vec(V)
         lib = _lib.load()
+        ctx.save_for_backward(Q, K, V, O, L)
+        ctx.is_causal = is_causal
+        ctx.scale = sm_scale
+        if not fast:
+            with torch.cuda.device(Q.device):
+                _lib.check(lib.mi_fa2_fwd_general(
+                    _lib.GENERAL_DTYPES[Q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                    O.data_ptr(), L.data_ptr(),
+                    kv_lens.data_ptr() if kv_lens is not None else None,
+                    batch_size, num_heads, num_kv_heads, seq_len, seq_len_k, d, d_v,
+                    _strides(q), _strides(k), _strides(v), _strides(O), _strides(L),
+                    int(bool(is_causal)), sm_scale, _lib.stream_of(Q)))
+            return O
         nbytes = lib.mi_fa2_fwd_workspace_size(batch_size, num_heads, num_kv_heads, seq_len,
                                                seq_len_k, d)
         ws = _workspace(nbytes, Q.device)
@@ -122,10 +157,6 @@ class FlashAttention2Function(torch.autograd.Function):
                 _strides(q), _strides(k), _strides(v), _strides(O), _strides(L),
                 int(bool(is_causal)), sm_scale,
                 ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _lib.stream_of(Q)))
-
-        ctx.save_for_backward(Q, K, V, O, L)
-        ctx.is_causal = is_causal
-        ctx.scale = sm_scale
         return O
 
 

@@ -22,7 +22,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     names = declared_symbols()
-    assert len(names) == 16
+    assert len(names) == 17
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_lib.SIGNATURES)
@@ -81,6 +81,55 @@ def test_c_abi_rejects_bad_arguments_before_any_launch(over, status, msg):
     lib = _lib.load()
     assert _fwd(lib, **over) == status
     assert msg in lib.mi_fa2_last_error().decode()
+
+
+def _fwd_general(lib, **over):
+    args = dict(dtype=2, q=16, k=16, v=16, o=16, batch=1, heads_q=4, heads_kv=2, seqlen_q=8,
+                seqlen_k=8, head_dim=64, head_dim_v=32)
+    args.update(over)
+    st = (ctypes.c_int64 * 4)(2048, 512, 64, 1)
+    return lib.mi_fa2_fwd_general(args["dtype"], args["q"], args["k"], args["v"], args["o"], None,
+                                  None, args["batch"], args["heads_q"], args["heads_kv"],
+                                  args["seqlen_q"], args["seqlen_k"], args["head_dim"],
+                                  args["head_dim_v"], st, st, st, st, None, 1, 0.125, None)
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(head_dim=8), 2, "power of two from 16 to 256"),
+    (dict(head_dim_v=512), 2, "power of two from 16 to 256"),
+    (dict(head_dim=48), 2, "power of two from 16 to 256"),
+    (dict(dtype=3), 2, "dtype"),
+    (dict(heads_q=6, heads_kv=4), 1, "bad sizes"),
+    (dict(batch=70000), 2, "65535"),
+    (dict(v=None), 1, "v is NULL"),
+    (dict(o=40), 1, "16-byte aligned"),
+])
+def test_general_entry_point_rejects_bad_arguments_before_any_launch(over, status, msg):
+    lib = _lib.load()
+    assert _fwd_general(lib, **over) == status
+    assert msg in lib.mi_fa2_last_error().decode()
+
+
+def test_general_entry_point_zero_sized_calls_are_no_ops():
+    lib = _lib.load()
+    assert _fwd_general(lib, batch=0) == 0
+    assert _fwd_general(lib, seqlen_q=0) == 0
+
+
+def test_python_mirror_routes_the_wider_envelope_and_rejects_the_rest():
+    # d and d_v powers of two (kernels/fa2.py:185) up to 256, bf16 / fp16 / fp32: accepted by the
+    # envelope checks (no launch here: these are CPU tensors, so the is_cuda assert fires first
+    # in apply; the envelope functions are checked directly).
+    q = torch.empty(1, 4, 3, 64)
+    fa2._general_envelope(q, torch.empty(1, 2, 5, 64), torch.empty(1, 2, 5, 256))
+    with pytest.raises(AssertionError):
+        fa2._general_envelope(torch.empty(1, 4, 3, 512), torch.empty(1, 2, 5, 512),
+                              torch.empty(1, 2, 5, 512))
+    with pytest.raises(AssertionError):
+        fa2._general_envelope(q.double(), torch.empty(1, 2, 5, 64).double(),
+                              torch.empty(1, 2, 5, 64).double())
+    with pytest.raises(AssertionError):
+        fa2._envelope(q.bfloat16(), q.bfloat16(), q.bfloat16())
 
 
 def test_paged_rejects_bad_block_size():

@@ -48,6 +48,25 @@ def test_sdpa_oracle_matches_fp64_brute_force(case):
     assert np.abs(got_lse[fin] - want_lse[fin]).max() < 2e-5
 
 
+@pytest.mark.parametrize("d,d_v", [(32, 64), (64, 16), (256, 32)])
+def test_sdpa_oracle_matches_fp64_brute_force_when_d_v_differs(d, d_v):
+    # The launcher takes V with its own head dim (kernels/fa2.py:172,185); the scale stays
+    # 1/sqrt(d) of Q and K (kernels/fa2.py:174).
+    g = torch.Generator().manual_seed(4)
+    B, Hq, Hkv, T, S, lens = 2, 4, 2, 5, 9, [9, 4]
+    q, k, v = _rand((B, Hq, T, d), g), _rand((B, Hkv, S, d), g), _rand((B, Hkv, S, d_v), g)
+    for causal in (True, False):
+        want, want_lse = brute.attention_f64(q, k, v, causal, lens)
+        got = sdpa.attention_ref(q, k, v, causal, lens)
+        assert got.shape == (B, Hq, T, d_v)
+        assert np.abs(got.numpy() - want).max() < 2e-6
+        fin = np.isfinite(want_lse)
+        assert np.abs(sdpa.lse_ref(q, k, causal, lens).numpy()[fin] - want_lse[fin]).max() < 2e-5
+    # planted mistake: a scale taken from V's head dim moves the output
+    bad, _ = brute.attention_f64(q * math.sqrt(d / d_v), k, v, True, lens)
+    assert np.abs(bad - brute.attention_f64(q, k, v, True, lens)[0]).max() > 1e-2
+
+
 def test_brute_force_matches_softmax_formula_at_full_head_dim():
     # d = 128 and GQA 6:1 as in the engine; compares against a vectorised textbook softmax.
     g = torch.Generator().manual_seed(2)
