@@ -4,18 +4,19 @@
 // bf16 / fp16, the shape the engine runs; this kernel is what every other shape runs on.
 //
 // Organisation (gfx950, wave64):
-//   * One wave = 16 query rows of one (row, query head); a work-group holds 4 waves on 4
-//     consecutive 16-row tiles.  No LDS and no barriers: each wave walks its own keys.
-//   * Keys go 16 at a time.  S^T = K Q^T on v_mfma_f32_16x16x16_{bf16,f16} (fp32: 16x16x4_f32, four
-//     per 16-wide slice of d) leaves lane l with query column l%16 and keys 4*(l/16) + r of the
-//     chunk, which is exactly the B-operand layout of O^T += V^T P^T: P never leaves registers.
-//     In every operand lane l holds 4 consecutive d (or 4 consecutive keys) of its row, so K and Q
-//     are 8- or 16-byte loads; V^T is gathered one element per key (adjacent lanes read adjacent
-//     d of one V row).
-//   * Online softmax as in kernels/fa2.py:136-150, in the exp2 domain (scale * log2(e) folded into
-//     the scores), the running max and sum per lane; the 4 lanes of a query exchange their chunk
-//     max with two xor shuffles.  P is rounded to the input type before the PV product
-//     (kernels/fa2.py:147: Pij.to(Vj.dtype)); fp32 inputs keep fp32 P and fp32 products
+//   * A work-group = 4 waves on 64 consecutive query rows (16 per wave) of one (row, query head).
+//     Each step stages 64 keys of K and V in LDS (16-byte loads, rows padded by 16 bytes), shared
+//     by the 4 waves; two barriers per step, no double buffering (several work-groups share a CU
+//     and cover each other's load latency).
+//   * S^T = K Q^T on v_mfma_f32_16x16x16_{bf16,f16} (fp32: four v_mfma_f32_16x16x4_f32 per
+//     16-wide slice of d), 16 keys per MFMA chunk, leaves lane l with query column l%16 and keys
+//     4*(l/16) + r of the chunk, which is exactly the B-operand layout of O^T += V^T P^T: P never
+//     leaves registers.  K operands are 8- or 16-byte LDS reads; V^T operands are transposing
+//     reads (ds_read_b64_tr_b16) for 16-bit types and 4-byte reads for fp32.
+//   * Online softmax as in kernels/fa2.py:136-150 once per 64 keys, in the exp2 domain (scale *
+//     log2(e) folded into the scores), the running max and sum per lane; the 4 lanes of a query
+//     exchange their max with two xor shuffles.  P is rounded to the input type before the PV
+//     product (kernels/fa2.py:147: Pij.to(Vj.dtype)); fp32 inputs keep fp32 P and fp32 products
 //     (input_precision="ieee", kernels/fa2.py:129,147).
 //   * Keys a query does not see (past its row's kv_len, or past the causal diagonal aligned to the
 //     row's last key, kernels/fa2.py:107-111,132-137) score -inf; K and V are not read past
@@ -26,6 +27,8 @@
 namespace mi_fa2 {
 
 struct F32 {};
+
+__device__ __forceinline__ u32x4 ld16_any(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 // Element traits: a "quad" is 4 consecutive elements of one row, the per-lane share of an operand
 // over a 16-wide slice of the contraction.
@@ -104,6 +107,26 @@ template <> struct Gen<F32> {
 
 constexpr int kGenWaves = 4;
 constexpr int kGenRows = 16;  // query rows per wave
+constexpr int kGenKeys = 64;  // keys staged in LDS per step: 4 chunks of 16
+
+// V^T operand of chunk c, d-block i out of the LDS V tile (row pitch VP): lane (m, g) holds
+// V[16c + 4g + j][16i + m] in element j.  16-bit: one ds_read_b64_tr_b16 (lane 4k+q of a 16-lane
+// group points at row 4g + k, columns 4q..4q+3, and receives column m of the 4 rows); fp32: four
+// 4-byte reads.
+template <class E, int VP>
+__device__ __forceinline__ typename Gen<E>::Quad gen_vt(const typename Gen<E>::T* vl, int c, int i,
+                                                        int lane) {
+  const int g = lane >> 4, m = lane & 15;
+  if constexpr (sizeof(typename Gen<E>::T) == 2) {
+    const int k = m >> 2, q = m & 3;
+    return __builtin_bit_cast(i16x4, ds_read_tr16(vl + (16 * c + 4 * g + k) * VP + 16 * i + 4 * q));
+  } else {
+    f32x4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = vl[(16 * c + 4 * g + j) * VP + 16 * i + m];
+    return r;
+  }
+}
 
 template <class E, int D, int DV>
 __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_kernel(FwdParams p) {
@@ -111,28 +134,41 @@ __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_kernel(FwdParams p
   using T = typename G::T;
   using Quad = typename G::Quad;
   constexpr int kDB = D / 16, kVB = DV / 16;
+  constexpr int kEl16 = 16 / sizeof(T);  // elements per 16-byte chunk
+  // LDS rows padded by one 16-byte chunk, so that the 16 rows an operand read touches start on
+  // different banks.
+  constexpr int KP = D + kEl16, VP = DV + kEl16;
+  __shared__ __attribute__((aligned(16))) T kl[kGenKeys * KP];
+  __shared__ __attribute__((aligned(16))) T vl[kGenKeys * VP];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
-  const int q0 = (blockIdx.x * kGenWaves + wave) * kGenRows;
   const int h = blockIdx.y, b = blockIdx.z;
-  if (q0 >= p.T) return;
   const int hk = h / p.group;
   const int kv_len = p.kv_lens ? clamp_len(p.kv_lens[b], p.S) : p.S;
   const int off = kv_len - p.T;  // query i sits at key position i + off
+  const int wg_q0 = blockIdx.x * kGenWaves * kGenRows;
+  const int q0 = wg_q0 + wave * kGenRows;
+  const bool wave_on = q0 < p.T;
   const int q = q0 + n;
-  const int q_last = min(q0 + kGenRows, p.T) - 1;
-  const int kv_hi = p.causal ? max(0, min(kv_len, q_last + off + 1)) : kv_len;
+  // Keys [0, hi) hold every key the queries up to q_last see.
+  auto keys_upto = [&](int q_last) {
+    return p.causal ? max(0, min(kv_len, q_last + off + 1)) : kv_len;
+  };
+  const int wave_hi = wave_on ? keys_upto(min(q0 + kGenRows, p.T) - 1) : 0;
+  const int wg_hi = keys_upto(min(wg_q0 + kGenWaves * kGenRows, p.T) - 1);
 
-  const T* qp = reinterpret_cast<const T*>(p.q) + b * p.q_sb + h * p.q_sh +
-                (int64_t)min(q, p.T - 1) * p.q_st;
   const T* kp = reinterpret_cast<const T*>(p.k) + b * p.k_sb + hk * p.k_sh;
   const T* vp = reinterpret_cast<const T*>(p.v) + b * p.v_sb + hk * p.v_sh;
 
   // Q^T as the B operand: lane (n, g) holds d = 16*s + 4*g .. +3 of query q for slice s.
   Quad qb[kDB];
+  {
+    const T* qp = reinterpret_cast<const T*>(p.q) + b * p.q_sb + h * p.q_sh +
+                  (int64_t)min(q, p.T - 1) * p.q_st;
 #pragma unroll
-  for (int s = 0; s < kDB; ++s) qb[s] = G::load(qp + 16 * s + 4 * g);
+    for (int s = 0; s < kDB; ++s) qb[s] = wave_on ? G::load(qp + 16 * s + 4 * g) : G::zero();
+  }
 
   f32x4 oacc[kVB];
 #pragma unroll
@@ -140,56 +176,87 @@ __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_kernel(FwdParams p
   float m_run = -INFINITY, l_run = 0.f;
   const float c = p.scale_log2;
 
-  for (int kc = 0; kc < kv_hi; kc += 16) {
-    // S^T[key][query]: K as the A operand, lane (n, g) = key kc + n, d = 16*s + 4*g .. +3.
-    const int kr = kc + n;
-    const bool k_ok = kr < kv_len;
-    const T* krow = kp + (int64_t)(k_ok ? kr : 0) * p.k_st + 4 * g;
-    f32x4 st = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < kDB; ++s) st = G::mma(k_ok ? G::load(krow + 16 * s) : G::zero(), qb[s], st);
-
-    // lane (n, g) now holds keys kc + 4*g + r of query q
-    float sc[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int key = kc + 4 * g + r;
-      const bool vis = key < kv_len && (!p.causal || key <= q + off);
-      sc[r] = vis ? st[r] * c : -INFINITY;
+  // Every wave runs the same steps (the barriers); a wave skips the compute of keys it does not see.
+  for (int kb = 0; kb < wg_hi; kb += kGenKeys) {
+    __syncthreads();  // the previous step's LDS reads are done
+    // K and V rows [kb, kb + 64) into LDS in 16-byte chunks; rows past kv_len are zeros (never
+    // loaded, so padding contents cannot reach the output).
+    constexpr int kKc = D / kEl16, kVc = DV / kEl16;
+#pragma unroll 4
+    for (int x = tid; x < kGenKeys * kKc; x += 64 * kGenWaves) {
+      const int r = x / kKc, ch = x - r * kKc;
+      u32x4 val = {0u, 0u, 0u, 0u};
+      if (kb + r < kv_len) val = ld16_any(kp + (int64_t)(kb + r) * p.k_st + ch * kEl16);
+      *reinterpret_cast<u32x4*>(kl + r * KP + ch * kEl16) = val;
     }
-    float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+#pragma unroll 4
+    for (int x = tid; x < kGenKeys * kVc; x += 64 * kGenWaves) {
+      const int r = x / kVc, ch = x - r * kVc;
+      u32x4 val = {0u, 0u, 0u, 0u};
+      if (kb + r < kv_len) val = ld16_any(vp + (int64_t)(kb + r) * p.v_st + ch * kEl16);
+      *reinterpret_cast<u32x4*>(vl + r * VP + ch * kEl16) = val;
+    }
+    __syncthreads();
+    if (kb >= wave_hi) continue;  // wave-uniform
+
+    // S^T of the 4 chunks: K as the A operand, lane (n, g) = key kb + 16*ch + n, d = 16*s + 4*g ..
+    // Chunks starting at or past wave_hi hold no key any of the wave's queries sees.
+    f32x4 st[4];
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch) {
+      st[ch] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (kb + 16 * ch < wave_hi) {
+        const T* kr = kl + (16 * ch + n) * KP + 4 * g;
+#pragma unroll
+        for (int s = 0; s < kDB; ++s) st[ch] = G::mma(G::load(kr + 16 * s), qb[s], st[ch]);
+      }
+    }
+    // lane (n, g) holds keys kb + 16*ch + 4*g + r of query q
+    float mx = -INFINITY;
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb + 16 * ch + 4 * g + r;
+        const bool vis = key < kv_len && (!p.causal || key <= q + off);
+        st[ch][r] = vis ? st[ch][r] * c : -INFINITY;
+        mx = fmaxf(mx, st[ch][r]);
+      }
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(m_run, mx);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = exp2_fast(m_run - m_use);
-    f32x4 pr;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) pr[r] = exp2_fast(sc[r] - m_use);
+    m_run = m_new;
     // The PV product takes P rounded to the input type (kernels/fa2.py:147); the row sum adds the
     // same rounded values, so that the weights applied to V sum to exactly 1 after the division.
     // (The reference sums P before rounding, kernels/fa2.py:145: in bf16 that leaves the weights
     // off by up to 2^-9 relative, which on outputs near 4 adds up to 8e-3 to the output's own
     // rounding.)  fp32: no rounding, the two are the same.
-    const Quad pq = G::pack(pr);
-    l_run = l_run * alpha + G::sum(pq);
-    m_run = m_new;
+    Quad pq[4];
+    float ls = 0.f;
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch) {
+      f32x4 pr;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pr[r] = exp2_fast(st[ch][r] - m_use);
+      pq[ch] = G::pack(pr);
+      ls += G::sum(pq[ch]);
+    }
+    l_run = l_run * alpha + ls;
 
-    // V^T as the A operand: lane (n, g) = d 16*i + n, keys kc + 4*g + j (j = element).  Keys past
-    // kv_len read as 0 (their address clamped to the row's last key, kv_len > 0 here).
+    // O^T += V^T P^T, d-block by d-block
 #pragma unroll
     for (int i = 0; i < kVB; ++i) {
-      Quad va;
+      f32x4 acc = oacc[i] * alpha;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int key = kc + 4 * g + j;
-        const T* vr = vp + (int64_t)min(key, kv_len - 1) * p.v_st + 16 * i + n;
-        va[j] = key < kv_len ? G::load1(vr) : 0;
-      }
-      oacc[i] = G::mma(va, pq, oacc[i] * alpha);
+      for (int ch = 0; ch < 4; ++ch)
+        if (kb + 16 * ch < wave_hi) acc = G::mma(gen_vt<E, VP>(vl, ch, i, lane), pq[ch], acc);
+      oacc[i] = acc;
     }
   }
 
+  if (!wave_on) return;
   // lane (n, g) holds the sums of keys 4*g + r of every chunk: the 4 lanes of a query add up.
   float l_tot = l_run + __shfl_xor(l_run, 16);
   l_tot += __shfl_xor(l_tot, 32);
