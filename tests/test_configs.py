@@ -4,7 +4,8 @@
   reference's plumbing case, run through its CPU SDPA fallback (model.py:104-107 with the mask
   choice of model.py:181-195).  On the CPU the model's fallback must equal the oracle (the
   reference's test oracle, kernels/test_fa2.py:28-35); on the GPU the bf16 cast of the same inputs
-  goes through FlashAttention2Function.apply and must meet the oracle's tolerance.
+  goes through FlashAttention2Function.apply and must meet the oracle's tolerance (the fp32
+  inputs themselves, on the general kernel, are checked in tests/test_fa2_general_gpu.py).
 * The end-to-end workload: the Qwen2.5-1.5B architecture at full size (28 layers, hidden 1536,
   SwiGLU 8960, vocab 151,936) with random N(0, 0.02) bf16 weights and a 1,024 x 16-token paged
   cache.  Its logits after two prompts and three decode steps must follow the same model with the
