@@ -47,8 +47,14 @@ def _vec(t):
 
 
 def _strides(t):
-    # a size-1 dimension is only ever indexed at 0, so its stride is irrelevant: pass 0
-    s = [0 if n == 1 else st for st, n in zip(t.stride(), t.shape)]
+    # A size-1 dimension is only ever indexed at 0, so its stride never moves an address, and torch
+    # may report any value there (0 after expand, anything after a view).  The kernels also use a
+    # token stride as the row pitch of their load extents (a load of `rows` rows reads at most
+    # rows * stride elements from the first row's start), so a size-1 dimension gets the stride it
+    # would have in a contiguous tensor: the product of the sizes after it, never less than the
+    # head dim.  (A 0 there made a single-token K or V read as zeros.)
+    s = [math.prod(t.shape[i + 1:]) if n == 1 else st
+         for i, (st, n) in enumerate(zip(t.stride(), t.shape))]
     return (_lib.ctypes.c_int64 * len(s))(*s)
 
 

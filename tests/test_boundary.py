@@ -155,10 +155,15 @@ def test_python_mirror_asserts_like_the_reference():
         fa2.FlashAttention2Function.apply(q, k, k, True, None)
 
 
-def test_stride_helper_zeroes_size_one_dims():
+def test_stride_helper_gives_size_one_dims_their_contiguous_stride():
+    # size-1 dims are indexed only at 0, but a token stride is also the row pitch of the kernels'
+    # load extents: it must cover a whole row (a 0 made a single-token K read as zeros)
     t = torch.empty(3, 1, 5, 128)[:, :, :, :]
-    s = list(fa2._strides(t))
-    assert s == [640, 0, 128, 1]
+    assert list(fa2._strides(t)) == [640, 640, 128, 1]
+    k = torch.empty(2, 2, 1, 128)
+    assert list(fa2._strides(k)) == [256, 128, 128, 1]
+    e = torch.empty(1, 2, 128).expand(1, 2, 128)
+    assert list(fa2._strides(e.as_strided((1, 2, 128), (0, 128, 1)))) == [256, 128, 1]
     assert fa2._dims_ok(torch.empty(2, 12, 7, 128))
     assert not fa2._dims_ok(torch.empty(2, 12, 7, 128).transpose(-1, -2))
 

@@ -429,6 +429,37 @@ def test_odd_query_counts(T):
     check_close(out, sdpa.attention_ref(q, k, v, True, lens), what=f"T={T}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_single_token_key_tensors(dtype):
+    """K and V of one token (S = 1, or a packed batch of one key in all): torch's stride for a
+    size-1 dimension is arbitrary, and the kernels take the token stride as the row pitch of their
+    load extents, so it is passed as the contiguous stride (a 0 there read the key as zeros)."""
+    g = torch.Generator().manual_seed(31)
+    for T, causal in ((1, False), (7, False), (7, True), (1, True)):
+        q = torch.randn(2, 12, T, 128, generator=g).to(dtype)
+        k = torch.randn(2, 2, 1, 128, generator=g).to(dtype)
+        v = torch.randn(2, 2, 1, 128, generator=g).to(dtype)
+        announce(f"[gpu] one key: T={T} causal={causal} {dtype}")
+        out = FlashAttention2Function.apply(q.to(DEV), k.to(DEV), v.to(DEV), causal, None)
+        torch.cuda.synchronize()
+        check_close(out, sdpa.attention_ref(q, k, v, causal), what=f"S=1 T={T} causal={causal}")
+    for qlens, klens in (([1], [1]), ([0, 1], [0, 1]), ([3, 0], [1, 0])):
+        cq, ck = [0], [0]
+        for a, b in zip(qlens, klens):
+            cq.append(cq[-1] + a)
+            ck.append(ck[-1] + b)
+        q = torch.randn(cq[-1], 12, 128, generator=g).to(dtype)
+        k = torch.randn(ck[-1], 2, 128, generator=g).to(dtype)
+        v = torch.randn(ck[-1], 2, 128, generator=g).to(dtype)
+        announce(f"[gpu] one key: packed qlens={qlens} klens={klens} {dtype}")
+        out = fa2_varlen(q.to(DEV), k.to(DEV), v.to(DEV),
+                         torch.tensor(cq, dtype=torch.int32, device=DEV),
+                         torch.tensor(ck, dtype=torch.int32, device=DEV), max(qlens),
+                         is_causal=False)
+        torch.cuda.synchronize()
+        check_close(out, sdpa.varlen_ref(q, k, v, cq, ck, False), what=f"packed {qlens}/{klens}")
+
+
 def test_mha_and_other_group_sizes():
     g = torch.Generator().manual_seed(12)
     for hq, hkv in [(4, 4), (16, 1), (32, 2)]:

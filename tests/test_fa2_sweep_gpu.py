@@ -1,0 +1,170 @@
+"""Seeded sweeps of the four attention entry points over shapes the targeted tests do not pin one by
+one: query / kv head counts from MHA to 32:1 groups (and kv head counts that do not divide 8),
+1 to 5 rows, a single query or up to 300, key counts from 0 to 400, causal or not, bf16 and fp16,
+paged block sizes 16 to 64, packed batches of 1 to 70 rows.  Each case is checked against the
+oracle; its parameters are printed before it runs.
+
+Bar: mean-abs < 1e-3, and every element within 1e-2 plus half an ulp of the output's own type at
+its magnitude (2^-8 |ref| for bf16, 2^-11 |ref| for fp16): queries that see one to three keys
+have outputs near single V values, which for N(0,1) data can exceed 4, where the rounding of the
+output alone is 1.6e-2 in bf16.
+"""
+import random
+
+import pytest
+import torch
+
+from conftest import announce
+from kernels.fa2 import FlashAttention2Function, fa2_paged, fa2_paged_varlen, fa2_varlen
+from oracle import paged as opaged
+from oracle import sdpa
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+HALF_ULP = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}
+
+
+def check(out, ref, dtype, what):
+    out = out.float().cpu()
+    ref = ref.float()
+    assert out.shape == ref.shape, (out.shape, ref.shape)
+    assert torch.isfinite(out).all(), f"{what}: non-finite output"
+    err = (out - ref).abs()
+    assert (err - (1e-2 + HALF_ULP[dtype] * ref.abs())).max().item() < 0, \
+        f"{what}: max-abs {err.max().item():.3e}"
+    assert err.mean().item() < 1e-3, f"{what}: mean-abs {err.mean().item():.3e}"
+
+
+def heads(rng):
+    hkv = rng.choice([1, 2, 3, 4, 5, 8])
+    group = rng.choice([g for g in (1, 2, 3, 5, 6, 7, 8, 12, 16, 24, 32) if hkv * g <= 64])
+    return hkv * group, hkv
+
+
+def qcount(rng):
+    return rng.choice([1, 1, rng.randint(2, 40), rng.randint(41, 300)])
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_padded_forward(seed):
+    rng = random.Random(1000 + seed)
+    g = torch.Generator().manual_seed(seed)
+    hq, hkv = heads(rng)
+    B, T, S = rng.randint(1, 5), qcount(rng), rng.randint(1, 400)
+    lens = [rng.choice([S, rng.randint(0, S)]) for _ in range(B)]
+    causal = rng.random() < 0.6
+    dtype = rng.choice([torch.bfloat16, torch.float16])
+    what = f"padded B={B} Hq={hq} Hkv={hkv} T={T} S={S} lens={lens} causal={causal} {dtype}"
+    announce(f"[gpu] sweep {what}")
+    q = torch.randn(B, hq, T, 128, generator=g).to(dtype)
+    k = torch.randn(B, hkv, S, 128, generator=g).to(dtype)
+    v = torch.randn(B, hkv, S, 128, generator=g).to(dtype)
+    out = FlashAttention2Function.apply(q.to(DEV), k.to(DEV), v.to(DEV), causal,
+                                        torch.tensor(lens, dtype=torch.int32, device=DEV))
+    torch.cuda.synchronize()
+    check(out, sdpa.attention_ref(q, k, v, causal, lens), dtype, what)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_packed_forward(seed):
+    rng = random.Random(2000 + seed)
+    g = torch.Generator().manual_seed(seed)
+    hq, hkv = heads(rng)
+    B = rng.choice([1, 2, rng.randint(3, 16), rng.randint(17, 70)])
+    qlens = [rng.choice([0, 1, rng.randint(1, 200)]) for _ in range(B)]
+    same = rng.random() < 0.5  # self-attention rows, or queries that are the last of their keys
+    klens = qlens if same else [n + rng.randint(0, 150) for n in qlens]
+    causal = rng.random() < 0.7
+    dtype = rng.choice([torch.bfloat16, torch.float16])
+    cq, ck = [0], [0]
+    for a, b in zip(qlens, klens):
+        cq.append(cq[-1] + a)
+        ck.append(ck[-1] + b)
+    if cq[-1] == 0:
+        qlens[0] = 1
+        klens[0] = max(klens[0], 1)
+        cq, ck = [0], [0]
+        for a, b in zip(qlens, klens):
+            cq.append(cq[-1] + a)
+            ck.append(ck[-1] + b)
+    what = f"packed B={B} Hq={hq} Hkv={hkv} qlens={qlens} klens={klens} causal={causal} {dtype}"
+    announce(f"[gpu] sweep {what}")
+    q = torch.randn(cq[-1], hq, 128, generator=g).to(dtype)
+    k = torch.randn(ck[-1], hkv, 128, generator=g).to(dtype)
+    v = torch.randn(ck[-1], hkv, 128, generator=g).to(dtype)
+    out = torch.full(q.shape, float("nan"), dtype=dtype, device=DEV)
+    fa2_varlen(q.to(DEV), k.to(DEV), v.to(DEV), torch.tensor(cq, dtype=torch.int32, device=DEV),
+               torch.tensor(ck, dtype=torch.int32, device=DEV), max(qlens), is_causal=causal,
+               out=out)
+    torch.cuda.synchronize()
+    check(out, sdpa.varlen_ref(q, k, v, cq, ck, causal), dtype, what)
+
+
+def _pool(lens, bs, g, hkv, dtype, spare):
+    num_blocks = sum(-(-n // bs) for n in lens) + spare
+    tables = opaged.random_tables(lens, bs, num_blocks, g)
+    kp = torch.randn(num_blocks * bs, hkv, 128, generator=g).to(dtype)
+    vp = torch.randn(num_blocks * bs, hkv, 128, generator=g).to(dtype)
+    return tables, kp, vp
+
+
+def _paged_ref(q, kp, vp, tables, lens, bs, causal):
+    S = max(max(lens), 1)
+    return sdpa.attention_ref(q, opaged.gather_dense(kp, tables, S, bs),
+                              opaged.gather_dense(vp, tables, S, bs), causal, lens)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_paged_forward(seed):
+    rng = random.Random(3000 + seed)
+    g = torch.Generator().manual_seed(seed)
+    hq, hkv = heads(rng)
+    B, T = rng.randint(1, 5), qcount(rng)
+    bs = rng.choice([16, 16, 32, 64])
+    lens = [rng.choice([T, T + rng.randint(0, 400)]) for _ in range(B)]
+    causal = T > 1
+    dtype = rng.choice([torch.bfloat16, torch.float16])
+    what = f"paged B={B} Hq={hq} Hkv={hkv} T={T} bs={bs} lens={lens} {dtype}"
+    announce(f"[gpu] sweep {what}")
+    tables, kp, vp = _pool(lens, bs, g, hkv, dtype, spare=rng.randint(0, 5))
+    q = torch.randn(B, hq, T, 128, generator=g).to(dtype)
+    out = fa2_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), opaged.table_tensor(tables).to(DEV),
+                    torch.tensor(lens, dtype=torch.int32, device=DEV), block_size=bs,
+                    is_causal=causal)
+    torch.cuda.synchronize()
+    check(out, _paged_ref(q, kp, vp, tables, lens, bs, causal), dtype, what)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_paged_packed_forward(seed):
+    rng = random.Random(4000 + seed)
+    g = torch.Generator().manual_seed(seed)
+    hq, hkv = heads(rng)
+    B = rng.randint(1, 12)
+    bs = rng.choice([16, 32, 64])
+    Ts = [rng.choice([0, 1, 1, rng.randint(2, 150)]) for _ in range(B)]
+    if sum(Ts) == 0:
+        Ts[0] = 1
+    lens = [t + rng.choice([0, rng.randint(0, 300)]) for t in Ts]
+    lens = [max(n, 1) for n in lens]
+    dtype = rng.choice([torch.bfloat16, torch.float16])
+    what = f"paged packed B={B} Hq={hq} Hkv={hkv} Ts={Ts} bs={bs} lens={lens} {dtype}"
+    announce(f"[gpu] sweep {what}")
+    tables, kp, vp = _pool(lens, bs, g, hkv, dtype, spare=2)
+    cu = [0]
+    for t in Ts:
+        cu.append(cu[-1] + t)
+    q = torch.randn(cu[-1], hq, 128, generator=g).to(dtype)
+    out = fa2_paged_varlen(q.to(DEV), kp.to(DEV), vp.to(DEV),
+                           torch.tensor(cu, dtype=torch.int32, device=DEV),
+                           opaged.table_tensor(tables).to(DEV),
+                           torch.tensor(lens, dtype=torch.int32, device=DEV), max(Ts),
+                           block_size=bs)
+    torch.cuda.synchronize()
+    for b, T in enumerate(Ts):
+        if T == 0:
+            continue
+        qb = q[cu[b]:cu[b + 1]].transpose(0, 1).unsqueeze(0)
+        ref = _paged_ref(qb, kp, vp, [tables[b]], [lens[b]], bs, True)
+        check(out[cu[b]:cu[b + 1]].transpose(0, 1).unsqueeze(0), ref, dtype, f"{what} row {b}")
