@@ -12,7 +12,9 @@
  * Conventions shared by every entry point
  *   - All pointers are device pointers except the stride arrays, which are host arrays.
  *   - Strides are in ELEMENTS, int64.  The innermost (head_dim) stride must be 1, every other stride
- *     a multiple of 8 elements and every tensor base 16-byte aligned (16-byte vector loads).
+ *     a multiple of 8 elements and every tensor base 16-byte aligned (16-byte vector loads).  The
+ *     token stride of K and V (the slot stride of a pool) is also the row pitch of their loads:
+ *     at least head_dim, also where seqlen_k is 1 (rows must not overlap).
  *   - `dtype` is MI_FA2_BF16 or MI_FA2_FP16; q, k, v and o share it (the sampler also takes
  *     MI_FA2_FP32 logits, mi_fa2_fwd_general MI_FA2_FP32 inputs).  Softmax and accumulation
  *     are fp32; `lse` is fp32 (natural log, like the reference's L, kernels/fa2.py:158,189).

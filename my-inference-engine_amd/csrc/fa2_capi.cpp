@@ -133,6 +133,15 @@ int check_tensor(const char* name, const void* ptr, const int64_t* strides, int 
   return MI_FA2_OK;
 }
 
+// K and V rows are loaded through buffer resources whose extent is (rows) x (token stride): a
+// token stride below the head dim would cut the last row short (and rows would overlap).
+int check_pitch(const char* name, int64_t token_stride) {
+  if (token_stride < mi_fa2::kHeadDim)
+    return fail(MI_FA2_ERR_INVALID, "%s token stride %lld is below head_dim %d (rows overlap)", name,
+                (long long)token_stride, mi_fa2::kHeadDim);
+  return MI_FA2_OK;
+}
+
 int launched(hipError_t err) {
   if (err != hipSuccess)
     return fail(MI_FA2_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
@@ -209,6 +218,7 @@ int fwd_paged(int32_t dtype, const void* q, const void* k_pool, const void* v_po
   if (int rc = check_tensor("o", o, o_strides, 3)) return rc;
   if (int rc = check_tensor("k_pool", k_pool, pool_strides, 2)) return rc;
   if (int rc = check_tensor("v_pool", v_pool, pool_strides, 2)) return rc;
+  if (int rc = check_pitch("pool", pool_strides[0])) return rc;
   if (lse && !lse_strides) return fail(MI_FA2_ERR_INVALID, "lse strides are NULL");
 
   FwdParams p{};
@@ -291,6 +301,8 @@ int mi_fa2_fwd(int32_t dtype, const void* q, const void* k, const void* v, void*
   if (seqlen_k > 0) {
     if (int rc = check_tensor("k", k, k_strides, 3)) return rc;
     if (int rc = check_tensor("v", v, v_strides, 3)) return rc;
+    if (int rc = check_pitch("k", k_strides[2])) return rc;
+    if (int rc = check_pitch("v", v_strides[2])) return rc;
   }
   if (lse && !lse_strides) return fail(MI_FA2_ERR_INVALID, "lse strides are NULL");
 
@@ -403,6 +415,8 @@ int mi_fa2_fwd_varlen(int32_t dtype, const void* q, const void* k, const void* v
   if (int rc = check_tensor("q", q, q_strides, 2)) return rc;
   if (int rc = check_tensor("k", k, k_strides, 2)) return rc;
   if (int rc = check_tensor("v", v, v_strides, 2)) return rc;
+  if (int rc = check_pitch("k", k_strides[0])) return rc;
+  if (int rc = check_pitch("v", v_strides[0])) return rc;
   if (int rc = check_tensor("o", o, o_strides, 2)) return rc;
   if (lse && !lse_strides) return fail(MI_FA2_ERR_INVALID, "lse strides are NULL");
 
@@ -486,6 +500,7 @@ int mi_fa2_fwd_paged_varlen(int32_t dtype, const void* q, const void* k_pool, co
   if (int rc = check_tensor("o", o, o_strides, 2)) return rc;
   if (int rc = check_tensor("k_pool", k_pool, pool_strides, 2)) return rc;
   if (int rc = check_tensor("v_pool", v_pool, pool_strides, 2)) return rc;
+  if (int rc = check_pitch("pool", pool_strides[0])) return rc;
   if (lse && !lse_strides) return fail(MI_FA2_ERR_INVALID, "lse strides are NULL");
 
   FwdParams p{};

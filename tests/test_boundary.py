@@ -132,6 +132,19 @@ def test_python_mirror_routes_the_wider_envelope_and_rejects_the_rest():
         fa2._envelope(q.bfloat16(), q.bfloat16(), q.bfloat16())
 
 
+def test_overlapping_key_rows_are_rejected():
+    lib = _lib.load()
+    st = (ctypes.c_int64 * 4)(8192, 1024, 128, 1)
+    kst = (ctypes.c_int64 * 4)(8192, 1024, 64, 1)
+    rc = lib.mi_fa2_fwd(0, 16, 16, 16, 16, None, None, 1, 12, 2, 8, 8, 128, st, kst, st, st, None,
+                        1, 0.1, None, 0, None)
+    assert rc == 1 and "below head_dim" in lib.mi_fa2_last_error().decode()
+    ps = (ctypes.c_int64 * 2)(64, 128)
+    rc = lib.mi_fa2_fwd_paged(0, 16, 16, 16, 16, None, 16, 8, 16, 1, 12, 2, 1, 64, 128, 16, 10,
+                              st, ps, st, None, 0, 0.1, None, 0, None)
+    assert rc == 1 and "below head_dim" in lib.mi_fa2_last_error().decode()
+
+
 def test_paged_rejects_bad_block_size():
     lib = _lib.load()
     st = (ctypes.c_int64 * 4)(1536, 128, 1536, 1)
