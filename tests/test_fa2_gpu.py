@@ -473,6 +473,21 @@ def test_mha_and_other_group_sizes():
             check_close(out, sdpa.attention_ref(q, k, v, True), what=f"{hq}/{hkv} T={T}")
 
 
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_single_head_short_rows(causal):
+    # One query head over one kv head (the item map's branch for fewer classes than XCDs), rows
+    # shorter than one 64-key tile, partly filled last tiles.
+    g = torch.Generator().manual_seed(14)
+    for B, T, S in ((1, 50, 50), (1, 50, 77), (3, 17, 50)):
+        q = torch.randn(B, 1, T, 128, generator=g).to(torch.bfloat16)
+        k = torch.randn(B, 1, S, 128, generator=g).to(torch.bfloat16)
+        v = torch.randn(B, 1, S, 128, generator=g).to(torch.bfloat16)
+        announce(f"[gpu] single head B={B} T={T} S={S} causal={causal}")
+        out = FlashAttention2Function.apply(q.to(DEV), k.to(DEV), v.to(DEV), causal, None)
+        torch.cuda.synchronize()
+        check_close(out, sdpa.attention_ref(q, k, v, causal), what=f"1/1 B={B} T={T} S={S}")
+
+
 def test_repeat_calls_are_bitwise_deterministic():
     q, k, v = wl.prefill_single(1024, seed=13)
     q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
