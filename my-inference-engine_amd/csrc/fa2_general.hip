@@ -43,6 +43,10 @@ template <> struct Gen<BF16> {
   static __device__ __forceinline__ f32x4 mma(const Quad& a, const Quad& b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
   }
+  // 16x16x32: k-slots 8*(l/16) .. +7 of lane l, eight elements (a0 then a1 for two quads)
+  static __device__ __forceinline__ f32x4 mma8(const u32x4& a, const u32x4& b, f32x4 c) {
+    return BF16::mfma16(a, b, c);
+  }
   static __device__ __forceinline__ T cvt(float x) {
     return __builtin_bit_cast(uint16_t, (__bf16)x);
   }
@@ -70,6 +74,9 @@ template <> struct Gen<FP16> {
   static __device__ __forceinline__ f32x4 mma(const Quad& a, const Quad& b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a),
                                                  __builtin_bit_cast(h4, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma8(const u32x4& a, const u32x4& b, f32x4 c) {
+    return FP16::mfma16(a, b, c);
   }
   static __device__ __forceinline__ T cvt(float x) {
     return __builtin_bit_cast(uint16_t, (_Float16)x);
@@ -133,7 +140,11 @@ __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_kernel(FwdParams p
   using G = Gen<E>;
   using T = typename G::T;
   using Quad = typename G::Quad;
-  constexpr int kDB = D / 16, kVB = DV / 16;
+  constexpr bool k16 = sizeof(T) == 2;
+  // 16-bit types with d >= 32 take the scores on v_mfma_f32_16x16x32 (8 consecutive d per lane:
+  // 16-byte operands); d = 16 and fp32 on 16-wide slices.
+  constexpr bool kOct = k16 && D >= 32;
+  constexpr int kDB = D / 16, kVB = DV / 16, kDO = D / 32;
   constexpr int kEl16 = 16 / sizeof(T);  // elements per 16-byte chunk
   // LDS rows padded by one 16-byte chunk, so that the 16 rows an operand read touches start on
   // different banks.
@@ -161,13 +172,20 @@ __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_kernel(FwdParams p
   const T* kp = reinterpret_cast<const T*>(p.k) + b * p.k_sb + hk * p.k_sh;
   const T* vp = reinterpret_cast<const T*>(p.v) + b * p.v_sb + hk * p.v_sh;
 
-  // Q^T as the B operand: lane (n, g) holds d = 16*s + 4*g .. +3 of query q for slice s.
-  Quad qb[kDB];
+  // Q^T as the B operand of the scores: lane (n, g) holds d = 32*s + 8*g .. +7 (kOct) or
+  // d = 16*s + 4*g .. +3 of query q.
+  u32x4 qo[kOct ? kDO : 1];
+  Quad qb[kOct ? 1 : kDB];
   {
     const T* qp = reinterpret_cast<const T*>(p.q) + b * p.q_sb + h * p.q_sh +
                   (int64_t)min(q, p.T - 1) * p.q_st;
+    if constexpr (kOct) {
 #pragma unroll
-    for (int s = 0; s < kDB; ++s) qb[s] = wave_on ? G::load(qp + 16 * s + 4 * g) : G::zero();
+      for (int s = 0; s < kDO; ++s) qo[s] = wave_on ? ld16_any(qp + 32 * s + 8 * g) : u32x4{};
+    } else {
+#pragma unroll
+      for (int s = 0; s < kDB; ++s) qb[s] = wave_on ? G::load(qp + 16 * s + 4 * g) : G::zero();
+    }
   }
 
   f32x4 oacc[kVB];
@@ -176,39 +194,89 @@ __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_kernel(FwdParams p
   float m_run = -INFINITY, l_run = 0.f;
   const float c = p.scale_log2;
 
+  // K and V rows [kb, kb + 64) in 16-byte chunks; rows past kv_len are zeros (never loaded, so
+  // padding contents cannot reach the output).  When a step's K and V fit 32 KB, the next step's
+  // chunks are loaded into registers while this step computes (8 VGPRs per KB... at most 32).
+  constexpr int kKc = D / kEl16, kVc = DV / kEl16;  // chunks per row
+  constexpr int kThreads = 64 * kGenWaves;
+  constexpr int kNK = (kGenKeys * kKc + kThreads - 1) / kThreads;
+  constexpr int kNV = (kGenKeys * kVc + kThreads - 1) / kThreads;
+  constexpr bool kPrefetch = (D + DV) * (int)sizeof(T) <= 512;
+  u32x4 nk[kPrefetch ? kNK : 1], nv[kPrefetch ? kNV : 1];
+  auto fetch = [&](int kb, u32x4* dk, u32x4* dv) {
+#pragma unroll
+    for (int i = 0; i < kNK; ++i) {
+      const int x = tid + kThreads * i, r = x / kKc, ch = x - r * kKc;
+      dk[i] = u32x4{0u, 0u, 0u, 0u};
+      if (x < kGenKeys * kKc && kb + r < kv_len)
+        dk[i] = ld16_any(kp + (int64_t)(kb + r) * p.k_st + ch * kEl16);
+    }
+#pragma unroll
+    for (int i = 0; i < kNV; ++i) {
+      const int x = tid + kThreads * i, r = x / kVc, ch = x - r * kVc;
+      dv[i] = u32x4{0u, 0u, 0u, 0u};
+      if (x < kGenKeys * kVc && kb + r < kv_len)
+        dv[i] = ld16_any(vp + (int64_t)(kb + r) * p.v_st + ch * kEl16);
+    }
+  };
+  auto commit = [&](const u32x4* dk, const u32x4* dv) {
+#pragma unroll
+    for (int i = 0; i < kNK; ++i) {
+      const int x = tid + kThreads * i, r = x / kKc, ch = x - r * kKc;
+      if (x < kGenKeys * kKc) *reinterpret_cast<u32x4*>(kl + r * KP + ch * kEl16) = dk[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kNV; ++i) {
+      const int x = tid + kThreads * i, r = x / kVc, ch = x - r * kVc;
+      if (x < kGenKeys * kVc) *reinterpret_cast<u32x4*>(vl + r * VP + ch * kEl16) = dv[i];
+    }
+  };
+  if constexpr (kPrefetch) {
+    if (wg_hi > 0) fetch(0, nk, nv);
+  }
+
   // Every wave runs the same steps (the barriers); a wave skips the compute of keys it does not see.
   for (int kb = 0; kb < wg_hi; kb += kGenKeys) {
     __syncthreads();  // the previous step's LDS reads are done
-    // K and V rows [kb, kb + 64) into LDS in 16-byte chunks; rows past kv_len are zeros (never
-    // loaded, so padding contents cannot reach the output).
-    constexpr int kKc = D / kEl16, kVc = DV / kEl16;
-#pragma unroll 4
-    for (int x = tid; x < kGenKeys * kKc; x += 64 * kGenWaves) {
-      const int r = x / kKc, ch = x - r * kKc;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (kb + r < kv_len) val = ld16_any(kp + (int64_t)(kb + r) * p.k_st + ch * kEl16);
-      *reinterpret_cast<u32x4*>(kl + r * KP + ch * kEl16) = val;
-    }
-#pragma unroll 4
-    for (int x = tid; x < kGenKeys * kVc; x += 64 * kGenWaves) {
-      const int r = x / kVc, ch = x - r * kVc;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (kb + r < kv_len) val = ld16_any(vp + (int64_t)(kb + r) * p.v_st + ch * kEl16);
-      *reinterpret_cast<u32x4*>(vl + r * VP + ch * kEl16) = val;
+    if constexpr (kPrefetch) {
+      commit(nk, nv);
+    } else {
+      // one chunk per thread at a time, straight from global memory to LDS
+      for (int x = tid; x < kGenKeys * kKc; x += kThreads) {
+        const int r = x / kKc, ch = x - r * kKc;
+        u32x4 val = {0u, 0u, 0u, 0u};
+        if (kb + r < kv_len) val = ld16_any(kp + (int64_t)(kb + r) * p.k_st + ch * kEl16);
+        *reinterpret_cast<u32x4*>(kl + r * KP + ch * kEl16) = val;
+      }
+      for (int x = tid; x < kGenKeys * kVc; x += kThreads) {
+        const int r = x / kVc, ch = x - r * kVc;
+        u32x4 val = {0u, 0u, 0u, 0u};
+        if (kb + r < kv_len) val = ld16_any(vp + (int64_t)(kb + r) * p.v_st + ch * kEl16);
+        *reinterpret_cast<u32x4*>(vl + r * VP + ch * kEl16) = val;
+      }
     }
     __syncthreads();
+    if constexpr (kPrefetch) {
+      if (kb + kGenKeys < wg_hi) fetch(kb + kGenKeys, nk, nv);  // in flight during this step
+    }
     if (kb >= wave_hi) continue;  // wave-uniform
 
-    // S^T of the 4 chunks: K as the A operand, lane (n, g) = key kb + 16*ch + n, d = 16*s + 4*g ..
+    // S^T of the 4 chunks: K as the A operand, lane (n, g) = key kb + 16*ch + n.
     // Chunks starting at or past wave_hi hold no key any of the wave's queries sees.
     f32x4 st[4];
 #pragma unroll
     for (int ch = 0; ch < 4; ++ch) {
       st[ch] = f32x4{0.f, 0.f, 0.f, 0.f};
       if (kb + 16 * ch < wave_hi) {
-        const T* kr = kl + (16 * ch + n) * KP + 4 * g;
+        const T* kr = kl + (16 * ch + n) * KP;
+        if constexpr (kOct) {
 #pragma unroll
-        for (int s = 0; s < kDB; ++s) st[ch] = G::mma(G::load(kr + 16 * s), qb[s], st[ch]);
+          for (int s = 0; s < kDO; ++s)
+            st[ch] = G::mma8(*reinterpret_cast<const u32x4*>(kr + 32 * s + 8 * g), qo[s], st[ch]);
+        } else {
+#pragma unroll
+          for (int s = 0; s < kDB; ++s) st[ch] = G::mma(G::load(kr + 16 * s + 4 * g), qb[s], st[ch]);
+        }
       }
     }
     // lane (n, g) holds keys kb + 16*ch + 4*g + r of query q
@@ -245,13 +313,29 @@ __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_kernel(FwdParams p
     }
     l_run = l_run * alpha + ls;
 
-    // O^T += V^T P^T, d-block by d-block
+    // O^T += V^T P^T, d-block by d-block.  16-bit: chunks in pairs on v_mfma_f32_16x16x32, k-slots
+    // 8g + j holding key 4g + j of the first chunk (j < 4) and of the second (j >= 4) in both
+    // operands; a pair is skipped when its first chunk is (the second then holds P = 0 rows).
 #pragma unroll
     for (int i = 0; i < kVB; ++i) {
       f32x4 acc = oacc[i] * alpha;
+      if constexpr (k16) {
 #pragma unroll
-      for (int ch = 0; ch < 4; ++ch)
-        if (kb + 16 * ch < wave_hi) acc = G::mma(gen_vt<E, VP>(vl, ch, i, lane), pq[ch], acc);
+        for (int pr2 = 0; pr2 < 2; ++pr2)
+          if (kb + 32 * pr2 < wave_hi) {
+            const i16x4 a0 = gen_vt<E, VP>(vl, 2 * pr2, i, lane);
+            const i16x4 a1 = gen_vt<E, VP>(vl, 2 * pr2 + 1, i, lane);
+            const u32x2 a0w = __builtin_bit_cast(u32x2, a0), a1w = __builtin_bit_cast(u32x2, a1);
+            const u32x2 b0w = __builtin_bit_cast(u32x2, pq[2 * pr2]);
+            const u32x2 b1w = __builtin_bit_cast(u32x2, pq[2 * pr2 + 1]);
+            acc = G::mma8(u32x4{a0w[0], a0w[1], a1w[0], a1w[1]},
+                          u32x4{b0w[0], b0w[1], b1w[0], b1w[1]}, acc);
+          }
+      } else {
+#pragma unroll
+        for (int ch = 0; ch < 4; ++ch)
+          if (kb + 16 * ch < wave_hi) acc = G::mma(gen_vt<E, VP>(vl, ch, i, lane), pq[ch], acc);
+      }
       oacc[i] = acc;
     }
   }
