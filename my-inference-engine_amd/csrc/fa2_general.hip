@@ -355,6 +355,170 @@ __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_kernel(FwdParams p
         l_tot > 0.f ? (m_run + __builtin_log2f(l_tot)) * kLn2 : -INFINITY;
 }
 
+// Key-split variant for launches that would leave the chip idle: fewer query rows than a
+// work-group of fa2_general_kernel holds (decode-shaped calls), or fewer of those work-groups
+// than CUs (a short sequence with few heads).  A work-group = 4 waves on the SAME 16 query rows;
+// wave w walks the w-th quarter of the 32-key pairs those rows see, loading its K and V operands
+// straight from global memory (no LDS, no barrier in the loop), and the 4 waves' (m, l, O) are
+// merged through LDS at the end, each wave finishing every 4th d-block.
+template <class E, int D, int DV>
+__global__ __launch_bounds__(64 * kGenWaves) void fa2_general_split_kernel(FwdParams p) {
+  using G = Gen<E>;
+  using T = typename G::T;
+  using Quad = typename G::Quad;
+  constexpr bool k16 = sizeof(T) == 2;
+  constexpr bool kOct = k16 && D >= 32;
+  constexpr int kDB = D / 16, kVB = DV / 16, kDO = D / 32;
+  __shared__ float sm_m[kGenWaves][kGenRows];
+  __shared__ float sm_l[kGenWaves][kGenRows];
+  __shared__ f32x4 sm_o[kGenWaves][kVB][64];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int hk = h / p.group;
+  const int kv_len = p.kv_lens ? clamp_len(p.kv_lens[b], p.S) : p.S;
+  const int off = kv_len - p.T;  // query i sits at key position i + off
+  const int q0 = blockIdx.x * kGenRows;
+  const int q = q0 + n;
+  const int q_last = min(q0 + kGenRows, p.T) - 1;
+  const int hi = p.causal ? max(0, min(kv_len, q_last + off + 1)) : kv_len;
+  // this wave's 32-key pairs
+  const int n_pairs = (hi + 31) >> 5;
+  const int pr_lo = wave * n_pairs / kGenWaves, pr_hi = (wave + 1) * n_pairs / kGenWaves;
+
+  const T* kp = reinterpret_cast<const T*>(p.k) + b * p.k_sb + hk * p.k_sh;
+  const T* vp = reinterpret_cast<const T*>(p.v) + b * p.v_sb + hk * p.v_sh;
+
+  u32x4 qo[kOct ? kDO : 1];
+  Quad qb[kOct ? 1 : kDB];
+  {
+    const T* qp = reinterpret_cast<const T*>(p.q) + b * p.q_sb + h * p.q_sh +
+                  (int64_t)min(q, p.T - 1) * p.q_st;
+    if constexpr (kOct) {
+#pragma unroll
+      for (int s = 0; s < kDO; ++s) qo[s] = ld16_any(qp + 32 * s + 8 * g);
+    } else {
+#pragma unroll
+      for (int s = 0; s < kDB; ++s) qb[s] = G::load(qp + 16 * s + 4 * g);
+    }
+  }
+
+  f32x4 oacc[kVB];
+#pragma unroll
+  for (int i = 0; i < kVB; ++i) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+  const float c = p.scale_log2;
+
+  for (int pr = pr_lo; pr < pr_hi; ++pr) {
+    const int kb = 32 * pr;
+    // S^T of the two 16-key chunks: K as the A operand straight from global memory (rows past
+    // kv_len read as zero operands, their address clamped to row 0).
+    f32x4 st[2];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      const int kr = kb + 16 * ch + n;
+      const bool k_ok = kr < kv_len;
+      const T* krow = kp + (int64_t)(k_ok ? kr : 0) * p.k_st;
+      st[ch] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (kOct) {
+#pragma unroll
+        for (int s = 0; s < kDO; ++s)
+          st[ch] = G::mma8(k_ok ? ld16_any(krow + 32 * s + 8 * g) : u32x4{}, qo[s], st[ch]);
+      } else {
+#pragma unroll
+        for (int s = 0; s < kDB; ++s)
+          st[ch] = G::mma(k_ok ? G::load(krow + 16 * s + 4 * g) : G::zero(), qb[s], st[ch]);
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb + 16 * ch + 4 * g + r;
+        const bool vis = key < kv_len && (!p.causal || key <= q + off);
+        st[ch][r] = vis ? st[ch][r] * c : -INFINITY;
+        mx = fmaxf(mx, st[ch][r]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2_fast(m_run - m_use);
+    m_run = m_new;
+    Quad pq[2];
+    float ls = 0.f;
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      f32x4 prb;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) prb[r] = exp2_fast(st[ch][r] - m_use);
+      pq[ch] = G::pack(prb);
+      ls += G::sum(pq[ch]);  // P as rounded for the PV product (see fa2_general_kernel)
+    }
+    l_run = l_run * alpha + ls;
+
+    // V^T as the A operand, gathered from global memory: element j of chunk ch is
+    // V[kb + 16*ch + 4*g + j][16*i + n] (rows past kv_len read as 0, address clamped).
+#pragma unroll
+    for (int i = 0; i < kVB; ++i) {
+      Quad va[2];
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = kb + 16 * ch + 4 * g + j;
+          const T* vr = vp + (int64_t)min(key, kv_len - 1) * p.v_st + 16 * i + n;
+          va[ch][j] = key < kv_len ? G::load1(vr) : 0;
+        }
+      f32x4 acc = oacc[i] * alpha;
+      if constexpr (k16) {
+        const u32x2 a0 = __builtin_bit_cast(u32x2, va[0]), a1 = __builtin_bit_cast(u32x2, va[1]);
+        const u32x2 b0 = __builtin_bit_cast(u32x2, pq[0]), b1 = __builtin_bit_cast(u32x2, pq[1]);
+        acc = G::mma8(u32x4{a0[0], a0[1], a1[0], a1[1]}, u32x4{b0[0], b0[1], b1[0], b1[1]}, acc);
+      } else {
+        acc = G::mma(va[0], pq[0], acc);
+        acc = G::mma(va[1], pq[1], acc);
+      }
+      oacc[i] = acc;
+    }
+  }
+
+  // Merge the 4 waves: lane (n, g) of every wave holds d = 16*i + 4*g + r of query q0 + n.
+  float l_w = l_run + __shfl_xor(l_run, 16);
+  l_w += __shfl_xor(l_w, 32);
+  if (g == 0) {
+    sm_m[wave][n] = m_run;
+    sm_l[wave][n] = l_w;
+  }
+#pragma unroll
+  for (int i = 0; i < kVB; ++i) sm_o[wave][i][lane] = oacc[i];
+  __syncthreads();
+  float M = sm_m[0][n];
+#pragma unroll
+  for (int u = 1; u < kGenWaves; ++u) M = fmaxf(M, sm_m[u][n]);
+  const float M_use = M == -INFINITY ? 0.f : M;
+  float f[kGenWaves], L = 0.f;
+#pragma unroll
+  for (int u = 0; u < kGenWaves; ++u) {
+    f[u] = exp2_fast(sm_m[u][n] - M_use);
+    L += f[u] * sm_l[u][n];
+  }
+  if (q >= p.T) return;
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  T* op = reinterpret_cast<T*>(p.o) + b * p.o_sb + h * p.o_sh + (int64_t)q * p.o_st;
+  for (int i = wave; i < kVB; i += kGenWaves) {
+    f32x4 o = sm_o[0][i][lane] * f[0];
+#pragma unroll
+    for (int u = 1; u < kGenWaves; ++u) o += sm_o[u][i][lane] * f[u];
+    G::store(op + 16 * i + 4 * g, o * inv);
+  }
+  if (p.lse && wave == 0 && g == 0)
+    p.lse[b * p.l_sb + h * p.l_sh + (int64_t)q * p.l_st] =
+        L > 0.f ? (M + __builtin_log2f(L)) * kLn2 : -INFINITY;
+}
+
 }  // namespace mi_fa2
 
 namespace mi_fa2 {
@@ -364,6 +528,15 @@ namespace {
 template <class E, int D, int DV>
 hipError_t launch_general_t(const FwdParams& p, hipStream_t stream) {
   const int rows_per_wg = kGenWaves * kGenRows;
+  const int64_t tiles = (int64_t)((p.T + rows_per_wg - 1) / rows_per_wg) * p.Hq * p.B;
+  // Fewer query rows than a work-group holds, or fewer work-groups than MI355X's 256 CUs: split
+  // each 16-row tile's keys over 4 waves instead (4x the work-groups, a quarter of the chain).
+  if (p.T < rows_per_wg || tiles < 256) {
+    const dim3 grid((p.T + kGenRows - 1) / kGenRows, p.Hq, p.B);
+    hipLaunchKernelGGL((fa2_general_split_kernel<E, D, DV>), grid, dim3(64 * kGenWaves), 0,
+                       stream, p);
+    return hipGetLastError();
+  }
   const dim3 grid((p.T + rows_per_wg - 1) / rows_per_wg, p.Hq, p.B);
   hipLaunchKernelGGL((fa2_general_kernel<E, D, DV>), grid, dim3(64 * kGenWaves), 0, stream, p);
   return hipGetLastError();
