@@ -179,6 +179,35 @@ def test_long_rows_and_single_queries(dtype):
     check_close(out, sdpa.attention_ref(q2, k2, v2, True), dtype, "chunked MQA")
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+def test_both_work_splits(dtype, causal):
+    """The launcher picks the LDS-staged kernel (64 query rows per work-group, K/V shared by its 4
+    waves) when there are at least 64 query rows and 256 such work-groups, else the key-split one
+    (16 rows per work-group, keys split over its 4 waves): shapes on both sides of that line."""
+    g = torch.Generator().manual_seed(9)
+    for B, Hq, Hkv, T, S, d, d_v in ((4, 16, 4, 256, 300, 64, 64),     # 4*16*4 = 256: LDS-staged
+                                     (4, 16, 4, 256, 300, 32, 128),
+                                     (4, 15, 5, 256, 300, 64, 64),      # 4*15*4 = 240: key-split
+                                     (2, 8, 2, 63, 500, 128, 32)):      # 63 rows: key-split
+        if dtype != torch.float32 and d == d_v == 128:
+            continue
+        q = rand((B, Hq, T, d), g, dtype)
+        k = rand((B, Hkv, S, d), g, dtype)
+        v = rand((B, Hkv, S, d_v), g, dtype)
+        lens = [S, S - 37, T, 200][:B]
+        announce(f"[gpu] general: B={B} Hq={Hq} T={T} S={S} d={d} d_v={d_v} {dtype} causal={causal}")
+        out, lse = fa2_forward(q.to(DEV), k.to(DEV), v.to(DEV), causal,
+                               torch.tensor(lens, dtype=torch.int32, device=DEV), return_lse=True)
+        torch.cuda.synchronize()
+        check_close(out, sdpa.attention_ref(q, k, v, causal, lens), dtype, f"B={B} Hq={Hq} T={T}")
+        want = sdpa.lse_ref(q, k, causal, lens)
+        fin = torch.isfinite(want)
+        assert torch.equal(fin, torch.isfinite(lse.cpu()))
+        bar = 1e-4 if dtype == torch.float32 else math.log1p(2.0 ** -8) + 1e-3
+        assert (lse.cpu()[fin] - want[fin]).abs().max().item() < bar
+
+
 def test_general_kernel_is_deterministic():
     g = torch.Generator().manual_seed(8)
     q = rand((2, 6, 33, 64), g, torch.bfloat16).to(DEV)
