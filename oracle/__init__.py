@@ -19,10 +19,18 @@ reference):
   rope.apply_rope        rotate-half RoPE in the tensor dtype (model.py:58-65) and its cos/sin
   rope.rope_cos_sin      tables (model.py:151-155); rope.cache_write, the cache scatter
   rope.cache_write       (kv_cache.py:108-115).
+  sample.sample          last-position sampling (chat.py:103-107) as an exponential race over
+                         Philox4x32-10 uniforms (sample.philox4x32, sample.uniforms), float64.
+
+sdpa.attention_ref, sdpa.lse_ref and brute.attention_f64 take any head dim d for Q/K and d_v for
+V (the launcher's envelope, kernels/fa2.py:172,185) and any float dtype (computed in fp32 / fp64).
 
 The seeded workload generators are not part of the oracle: they live in the package
 (my-inference-engine_amd/workloads.py) because bench.py's GPU leg needs them too.
 
-Parity status: every function above is pinned by tests/test_oracle.py (fp64 brute force, closed
-forms, GQA/permutation/padding invariants).  None is "parity unpinned".
+Parity status: every function above is pinned: the attention and cache functions by
+tests/test_oracle.py (fp64 brute force, also with d_v != d; closed forms; GQA / permutation /
+padding invariants; planted mistakes), RoPE by tests/test_rope.py, the sampler by
+tests/test_sample.py (the Random123 known-answer vectors, chi-square against softmax(logits/T)).
+None is "parity unpinned".
 """
