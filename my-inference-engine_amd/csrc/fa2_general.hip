@@ -4,19 +4,22 @@
 // bf16 / fp16, the shape the engine runs; this kernel is what every other shape runs on.
 //
 // Organisation (gfx950, wave64):
-//   * A work-group = 4 waves on 64 consecutive query rows (16 per wave) of one (row, query head).
-//     Each step stages 64 keys of K and V in LDS (16-byte loads, rows padded by 16 bytes), shared
-//     by the 4 waves; two barriers per step, no double buffering (several work-groups share a CU
-//     and cover each other's load latency).
-//   * S^T = K Q^T on v_mfma_f32_16x16x16_{bf16,f16} (fp32: four v_mfma_f32_16x16x4_f32 per
-//     16-wide slice of d), 16 keys per MFMA chunk, leaves lane l with query column l%16 and keys
-//     4*(l/16) + r of the chunk, which is exactly the B-operand layout of O^T += V^T P^T: P never
-//     leaves registers.  K operands are 8- or 16-byte LDS reads; V^T operands are transposing
-//     reads (ds_read_b64_tr_b16) for 16-bit types and 4-byte reads for fp32.
-//   * Online softmax as in kernels/fa2.py:136-150 once per 64 keys, in the exp2 domain (scale *
-//     log2(e) folded into the scores), the running max and sum per lane; the 4 lanes of a query
-//     exchange their max with two xor shuffles.  P is rounded to the input type before the PV
-//     product (kernels/fa2.py:147: Pij.to(Vj.dtype)); fp32 inputs keep fp32 P and fp32 products
+//   * fa2_general_kernel: a work-group = 4 waves on 64 consecutive query rows (16 per wave) of one
+//     (row, query head).  Each step stages 64 keys of K and V in LDS (16-byte loads, rows padded
+//     by 16 bytes), shared by the 4 waves, two barriers per step; when a step fits 32 KB the next
+//     step's rows are loaded into registers while this one computes.
+//   * fa2_general_split_kernel, for launches that would leave CUs idle (fewer than 64 query rows,
+//     or fewer such work-groups than CUs): the 4 waves share 16 query rows and split their keys,
+//     loading K and V operands straight from global memory, and merge (m, l, O) through LDS.
+//   * S^T = K Q^T leaves lane l with query column l%16 and keys 4*(l/16) + r of a 16-key chunk,
+//     which is exactly the B-operand layout of O^T += V^T P^T: P never leaves registers.  16-bit
+//     types run both products on v_mfma_f32_16x16x32 (8 consecutive d per lane for the scores,
+//     d = 16 on 16x16x16; pairs of 16-key chunks for PV), fp32 on four v_mfma_f32_16x16x4_f32 per
+//     16-wide slice.  V^T operands come from ds_read_b64_tr_b16 (16-bit) or 4-byte reads (fp32).
+//   * Online softmax as in kernels/fa2.py:136-150, in the exp2 domain (scale * log2(e) folded into
+//     the scores), the running max and sum per lane; the 4 lanes of a query exchange their max
+//     with two xor shuffles.  P is rounded to the input type before the PV product
+//     (kernels/fa2.py:147: Pij.to(Vj.dtype)); fp32 inputs keep fp32 P and fp32 products
 //     (input_precision="ieee", kernels/fa2.py:129,147).
 //   * Keys a query does not see (past its row's kv_len, or past the causal diagonal aligned to the
 //     row's last key, kernels/fa2.py:107-111,132-137) score -inf; K and V are not read past
@@ -196,7 +199,8 @@ __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_kernel(FwdParams p
 
   // K and V rows [kb, kb + 64) in 16-byte chunks; rows past kv_len are zeros (never loaded, so
   // padding contents cannot reach the output).  When a step's K and V fit 32 KB, the next step's
-  // chunks are loaded into registers while this step computes (8 VGPRs per KB... at most 32).
+  // chunks are loaded into registers while this step computes (each thread holds 1/256 of the
+  // step: 4 VGPRs per 4 KB, at most 32 VGPRs).
   constexpr int kKc = D / kEl16, kVc = DV / kEl16;  // chunks per row
   constexpr int kThreads = 64 * kGenWaves;
   constexpr int kNK = (kGenKeys * kKc + kThreads - 1) / kThreads;
