@@ -91,7 +91,7 @@ MI_FA2_API int mi_fa2_fwd(int32_t dtype, const void* q, const void* k, const voi
  *   q [batch, heads_q, seqlen_q, head_dim], k [batch, heads_kv, seqlen_k, head_dim],
  *   v [batch, heads_kv, seqlen_k, head_dim_v], o [batch, heads_q, seqlen_q, head_dim_v];
  *   everything else as in mi_fa2_fwd (kv_lens clamped to [0, seqlen_k], bottom-right causal mask,
- *   lse may be NULL).  batch and heads_q are at most 65535.  One kernel (16x16 MFMAs, no LDS, no
+ *   lse may be NULL).  batch and heads_q are at most 65535.  One kernel family (16x16 MFMAs, no
  *   workspace) serves every seqlen_q; bf16/fp16 at head_dim = head_dim_v = 128 is faster through
  *   mi_fa2_fwd, which this entry point does not dispatch to.
  */
