@@ -6,8 +6,9 @@
  *   - its launcher `FlashAttention2Function`     (kernels/fa2.py:164-214),
  *   - the per-step dense K/V gather it is fed by (kv_cache.py:117-121, called at model.py:97),
  * with hand-written HIP kernels: an MFMA/LDS-tiled prefill kernel, a split-KV decode kernel that
- * reads K/V straight out of the paged cache's blocks, and a split combine kernel; and the steps
- * either side of it: a fused RoPE + paged cache write and a fused last-position token sampler.
+ * reads K/V straight out of the paged cache's blocks, and a split combine kernel (head_dim 128,
+ * bf16/fp16), a general kernel for the launcher's other head dims and fp32; and the steps either
+ * side of it: a fused RoPE + paged cache write and a fused last-position token sampler.
  *
  * Conventions shared by every entry point
  *   - All pointers are device pointers except the stride arrays, which are host arrays.
