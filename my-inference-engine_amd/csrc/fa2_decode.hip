@@ -15,9 +15,10 @@
 //     A operand (8 keys x 8 dims per lane), so nothing goes through LDS in the key loop.
 //   * Dense K/V: the key loop is software-pipelined, the loads of step s+1 in flight while step s
 //     is computed (two register buffers, 2 waves per SIMD).  Paged K/V: one buffer and 3 waves per
-//     SIMD; where a work-group's share crosses from one item to the next, the next item's q, first
-//     block-table entries and first K/V step are issued before this item's merge, so the merge
-//     runs under their latency (53.1 -> 51.3 us on 64 rows of U[128, 8192] keys).
+//     SIMD.  Both: where a work-group's share crosses from one item to the next, the next item's
+//     q, first K/V step (and, paged, its first block-table entries) are issued before this item's
+//     merge, so the merge runs under their latency (paged, 64 rows of U[128, 8192] keys: 53.1 ->
+//     51.3 us per step).
 //   * S^T = K Q^T leaves one query head per lane column and 4 keys per lane, which is the B-operand
 //     layout of O^T += V^T P^T: softmax state stays in registers.
 //   * The 4 waves' partial (m, l, O) are merged in LDS.  A row that fits in one split is finished in
@@ -329,83 +330,86 @@ __global__ __launch_bounds__(256, DcShape<MODE>::kOcc) void fa2_decode_kernel(co
   const int g = lane >> 4;  // lane group: k-slots 8g..8g+7
   const float cl = p.scale_log2;
 
+  const auto kv_len_of = [&](int bb) { return p.kv_lens ? clamp_len(p.kv_lens[bb], p.S) : p.S; };
+  const auto load_q = [&](int bb, int hh, u32x4 (&qb)[4]) {
+    if (n < p.group) {
+      const uint16_t* qp =
+          p.q + (int64_t)bb * p.q_sb + (int64_t)(hh * p.group + n) * p.q_sh + g * 8;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) qb[ks] = ld16(qp + ks * 32);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) qb[ks] = u32x4{0, 0, 0, 0};
+    }
+  };
+  const auto k_off_of = [&](int bb, int hh) {
+    return (MODE == kDense ? (int64_t)bb * p.k_sb : 0) + (int64_t)hh * p.k_sh;
+  };
+  const auto v_off_of = [&](int bb, int hh) {
+    return (MODE == kDense ? (int64_t)bb * p.v_sb : 0) + (int64_t)hh * p.v_sh;
+  };
   if constexpr (DcShape<MODE>::kPipe) {
-    while (lo < hi) {
-      const int c_end = (int)min<int64_t>(n_b, c + (hi - lo));
-      const int kv_len = p.kv_lens ? clamp_len(p.kv_lens[b], p.S) : p.S;
-      const int k_begin = c * kDcChunk;
-      const int k_end = min(kv_len, c_end * kDcChunk);
-
-      const int64_t k_off = (MODE == kDense ? (int64_t)b * p.k_sb : 0) + (int64_t)hk * p.k_sh;
-      const int64_t v_off = (MODE == kDense ? (int64_t)b * p.v_sb : 0) + (int64_t)hk * p.v_sh;
-
-      // Q^T as the B operand of S^T = K Q^T: k-step ks covers d = 32*ks + 8*g + [0, 8).
-      u32x4 qb[4];
-      if (n < p.group) {
-        const uint16_t* qp =
-            p.q + (int64_t)b * p.q_sb + (int64_t)(hk * p.group + n) * p.q_sh + g * 8;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) qb[ks] = ld16(qp + ks * 32);
-      } else {
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) qb[ks] = u32x4{0, 0, 0, 0};
+    // Dense walk, two register buffers: step s+1's loads fly during step s's math.  As in the
+    // paged walk below, the next item's q and first K/V step are issued before this item's merge.
+    int c_end = (int)min<int64_t>(n_b, c + (hi - lo));
+    int k_end = min(kv_len_of(b), c_end * kDcChunk);
+    int kb = c * kDcChunk + wave * kDcStep;
+    u32x4 qb[4];
+    load_q(b, hk, qb);
+    DcStep s0, s1;
+    if (kb < k_end) dc_load<MODE>(p, b, k_off_of(b, hk), v_off_of(b, hk), kb, k_end, n, g, 0, s0);
+    while (true) {
+      // The item after this one in the share (none: k_end2 = 0, so nothing is fetched for it).
+      const int64_t lo2 = lo + (c_end - c);
+      const bool more = lo2 < hi;
+      int b2 = b, hk2 = hk + 1, n_b2 = n_b;
+      if (hk2 == p.Hkv) {
+        hk2 = 0;
+        ++b2;
+        if (more) n_b2 = R[b2 + 1] - R[b2];
       }
+      const int c_end2 = more ? (int)min<int64_t>(n_b2, hi - lo2) : 0;
+      const int k_end2 = more ? min(kv_len_of(b2), c_end2 * kDcChunk) : 0;
+      const int kb2 = wave * kDcStep;
+      const int64_t k_off = k_off_of(b, hk);
+      const int64_t v_off = v_off_of(b, hk);
 
       f32x4 oacc[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) oacc[i] = f32x4{};
       float m_run = -INFINITY;
       float l_run = 0.f;
-
-      int kb = k_begin + wave * kDcStep;
-      {
-        // Two register buffers: step s+1's loads fly during step s's math.
-        DcStep s0, s1;
-        int tbl = dc_tbl_fetch<MODE>(p, b, kb, k_end, lane);
-        if (kb < k_end) dc_load<MODE>(p, b, k_off, v_off, kb, k_end, n, g, tbl, s0);
-        tbl = dc_tbl_fetch<MODE>(p, b, kb + kDcChunk, k_end, lane);
-        while (kb < k_end) {
-          const int kb1 = kb + kDcChunk;
-          if (kb1 < k_end) dc_load<MODE>(p, b, k_off, v_off, kb1, k_end, n, g, tbl, s1);
-          tbl = dc_tbl_fetch<MODE>(p, b, kb1 + kDcChunk, k_end, lane);
-          dc_compute<E>(s0, qb, kb, k_end, g, cl, m_run, l_run, oacc);
-          if (kb1 >= k_end) break;
-          const int kb2 = kb1 + kDcChunk;
-          if (kb2 < k_end) dc_load<MODE>(p, b, k_off, v_off, kb2, k_end, n, g, tbl, s0);
-          tbl = dc_tbl_fetch<MODE>(p, b, kb2 + kDcChunk, k_end, lane);
-          dc_compute<E>(s1, qb, kb1, k_end, g, cl, m_run, l_run, oacc);
-          kb = kb2;
-        }
+      while (kb < k_end) {
+        const int kb1 = kb + kDcChunk;
+        if (kb1 < k_end) dc_load<MODE>(p, b, k_off, v_off, kb1, k_end, n, g, 0, s1);
+        dc_compute<E>(s0, qb, kb, k_end, g, cl, m_run, l_run, oacc);
+        if (kb1 >= k_end) break;
+        const int kb3 = kb1 + kDcChunk;
+        if (kb3 < k_end) dc_load<MODE>(p, b, k_off, v_off, kb3, k_end, n, g, 0, s0);
+        dc_compute<E>(s1, qb, kb1, k_end, g, cl, m_run, l_run, oacc);
+        kb = kb3;
       }
-
+      if (more) {
+        load_q(b2, hk2, qb);
+        if (kb2 < k_end2)
+          dc_load<MODE>(p, b2, k_off_of(b2, hk2), v_off_of(b2, hk2), kb2, k_end2, n, g, 0, s0);
+      }
       dc_finish<E>(p, R, red_o, red_m, red_l, N, W, w, b, hk, c, c_end, n_b, wave, n, g, tid, oacc,
                    m_run, l_run);
-
-      // Next item.
-      lo += c_end - c;
+      if (!more) break;
+      lo = lo2;
       c = 0;
-      if (++hk == p.Hkv) {
-        hk = 0;
-        ++b;
-        if (b < p.B) n_b = R[b + 1] - R[b];
-      }
+      b = b2;
+      hk = hk2;
+      n_b = n_b2;
+      c_end = c_end2;
+      k_end = k_end2;
+      kb = kb2;
     }
   } else {
     // Paged walk, one register buffer.  The next item's q, its first block-table entries and its
     // first K/V step are issued before this item's merge (the table entries during this item's last
     // step), so a share that crosses an item boundary waits out no memory round trip between them.
-    const auto kv_len_of = [&](int bb) { return p.kv_lens ? clamp_len(p.kv_lens[bb], p.S) : p.S; };
-    const auto load_q = [&](int bb, int hh, u32x4 (&qb)[4]) {
-      if (n < p.group) {
-        const uint16_t* qp =
-            p.q + (int64_t)bb * p.q_sb + (int64_t)(hh * p.group + n) * p.q_sh + g * 8;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) qb[ks] = ld16(qp + ks * 32);
-      } else {
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) qb[ks] = u32x4{0, 0, 0, 0};
-      }
-    };
     int c_end = (int)min<int64_t>(n_b, c + (hi - lo));
     int k_end = min(kv_len_of(b), c_end * kDcChunk);
     int kb = c * kDcChunk + wave * kDcStep;
