@@ -418,8 +418,7 @@ __global__ __launch_bounds__(256, DcShape<MODE>::kOcc) void fa2_decode_kernel(co
     DcStep s;
     {
       const int t0 = dc_tbl_fetch<MODE>(p, b, kb, k_end, lane);
-      if (kb < k_end) dc_load<MODE>(p, b, (int64_t)hk * p.k_sh, (int64_t)hk * p.v_sh, kb, k_end, n,
-                                    g, t0, s);
+      if (kb < k_end) dc_load<MODE>(p, b, k_off_of(b, hk), v_off_of(b, hk), kb, k_end, n, g, t0, s);
     }
     while (true) {
       // The item after this one in the share (none: k_end2 = 0, so nothing is fetched for it).
@@ -440,8 +439,8 @@ __global__ __launch_bounds__(256, DcShape<MODE>::kOcc) void fa2_decode_kernel(co
         return kn < k_end ? dc_tbl_fetch<MODE>(p, b, kn, k_end, lane)
                           : dc_tbl_fetch<MODE>(p, b2, kb2, k_end2, lane);
       };
-      const int64_t k_off = (int64_t)hk * p.k_sh;
-      const int64_t v_off = (int64_t)hk * p.v_sh;
+      const int64_t k_off = k_off_of(b, hk);
+      const int64_t v_off = v_off_of(b, hk);
 
       f32x4 oacc[8];
 #pragma unroll
@@ -460,8 +459,7 @@ __global__ __launch_bounds__(256, DcShape<MODE>::kOcc) void fa2_decode_kernel(co
       if (more) {
         load_q(b2, hk2, qb);
         if (kb2 < k_end2)
-          dc_load<MODE>(p, b2, (int64_t)hk2 * p.k_sh, (int64_t)hk2 * p.v_sh, kb2, k_end2, n, g,
-                        tbl, s);
+          dc_load<MODE>(p, b2, k_off_of(b2, hk2), v_off_of(b2, hk2), kb2, k_end2, n, g, tbl, s);
       }
       dc_finish<E>(p, R, red_o, red_m, red_l, N, W, w, b, hk, c, c_end, n_b, wave, n, g, tid, oacc,
                    m_run, l_run);
