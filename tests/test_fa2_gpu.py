@@ -256,6 +256,32 @@ def test_paged_decode_equals_dense_decode_bitwise():
     assert torch.equal(o_dense.cpu(), o_paged.cpu())
 
 
+def test_decode_shares_crossing_many_items():
+    """300 short rows (0-700 keys, a few empty): about 1,800 128-key chunks over 768 (paged) or 512
+    (dense) work-groups, so most shares end inside one (row, kv head) item and go on into the next,
+    often into an empty row or one where only some waves have keys.  Those switches are where the
+    next item's q, table entries and first K/V step are issued before the current item's merge."""
+    q, kp, vp, tables, lens = wl.decode_paged(n_rows=300, lo=1, hi=700, seed=12)
+    lens = [0 if i % 37 == 5 else n for i, n in enumerate(lens)]
+    S = max(lens)
+    ref = _paged_ref(q, kp, vp, tables, lens, 16, False)
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    announce("[gpu] decode, 300 short rows: paged")
+    o_paged = fa2_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), wl.table_tensor(tables).to(DEV), lens_t,
+                        max_kv_len=S)
+    torch.cuda.synchronize()
+    check_close(o_paged, ref, what="paged decode, 300 short rows")
+    kd = opaged.gather_dense(kp, tables, S, 16).contiguous()
+    vd = opaged.gather_dense(vp, tables, S, 16).contiguous()
+    announce("[gpu] decode, 300 short rows: dense")
+    o_dense = FlashAttention2Function.apply(q.to(DEV), kd.to(DEV), vd.to(DEV), False, lens_t)
+    torch.cuda.synchronize()
+    check_close(o_dense, ref, what="dense decode, 300 short rows")
+    empty = [i for i, n in enumerate(lens) if n == 0]
+    assert torch.equal(o_paged[empty].cpu().float(), torch.zeros(len(empty), 12, 1, 128))
+    assert torch.equal(o_dense[empty].cpu().float(), torch.zeros(len(empty), 12, 1, 128))
+
+
 def test_paged_prefill_4096_equals_dense_prefill_bitwise():
     # The bench's paged prefill workload: the same kernel reading K/V through a permuted table of
     # 16-token blocks must give the dense kernel's bits on the gathered K/V.
