@@ -76,8 +76,10 @@ def _ramp(fn, ms):
 
 
 def _time_gpu(fn, steps, warmup, ramp_ms=None):
-    """Average ms per call of fn() over exactly `steps` calls, HIP events on the current stream,
-    after the sustained-clock ramp (`_ramp`) and `warmup` untimed calls.
+    """(average ms per call of fn() over exactly `steps` calls, the shader clock they ran at):
+    HIP events on the current stream, after the sustained-clock ramp (`_ramp`) and `warmup`
+    untimed calls.  Clock stamps (kernels.clock.ClockStamp) on the same stream right before the
+    start event and right after the end event give the clock of the timed calls, per XCD.
 
     Python's garbage collector is run first and disabled from the ramp to the end of the timed
     calls (as timeit does): the host enqueues a call in 35-50 us against a 50-70 us kernel, so a
@@ -85,6 +87,8 @@ def _time_gpu(fn, steps, warmup, ramp_ms=None):
     make one likely -- would leave the GPU idle inside it (seen: 0.7-1.05 ms per call instead of
     0.061), and one between the ramp and the timed calls would let the clock fall back."""
     import torch
+    from kernels.clock import ClockStamp
+    stamp = ClockStamp()
     gc.collect()
     enabled = gc.isenabled()
     gc.disable()
@@ -95,15 +99,17 @@ def _time_gpu(fn, steps, warmup, ramp_ms=None):
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
+        stamp.before()
         start.record()
         for i in range(steps):
             fn(i)
         end.record()
+        stamp.after()
         torch.cuda.synchronize()
     finally:
         if enabled:
             gc.enable()
-    return start.elapsed_time(end) / steps
+    return start.elapsed_time(end) / steps, stamp.result()
 
 
 def bench_prefill(steps, warmup, seq_len=4096, cold=False):
@@ -114,10 +120,10 @@ def bench_prefill(steps, warmup, seq_len=4096, cold=False):
     from kernels.fa2 import FlashAttention2Function
     q, k, v = (t.cuda() for t in wl.prefill_single(seq_len, seed=0))
     fn = lambda i=0: FlashAttention2Function.apply(q, k, v, True, None)
-    cold_ms = _time_gpu(fn, steps, warmup, ramp_ms=0.0) if cold else None
-    ms = _time_gpu(fn, steps, warmup)
+    cold_ms = _time_gpu(fn, steps, warmup, ramp_ms=0.0)[0] if cold else None
+    ms, clock = _time_gpu(fn, steps, warmup)
     flops = wl.causal_prefill_flops([seq_len])
-    return (ms, flops, cold_ms) if cold else (ms, flops)
+    return (ms, flops, clock, cold_ms) if cold else (ms, flops, clock)
 
 
 def bench_ragged(steps, warmup):
@@ -128,8 +134,9 @@ def bench_ragged(steps, warmup):
     q, k, v = q.cuda(), k.cuda(), v.cuda()
     cu_t = torch.tensor(cu, dtype=torch.int32, device="cuda")
     mx = max(lens)
-    ms = _time_gpu(lambda i=0: fa2_varlen(q, k, v, cu_t, cu_t, mx, is_causal=True), steps, warmup)
-    return ms, wl.causal_prefill_flops(lens), lens
+    ms, clock = _time_gpu(lambda i=0: fa2_varlen(q, k, v, cu_t, cu_t, mx, is_causal=True), steps,
+                          warmup)
+    return ms, wl.causal_prefill_flops(lens), lens, clock
 
 
 def bench_paged_prefill(steps, warmup, seq_len=4096):
@@ -142,9 +149,9 @@ def bench_paged_prefill(steps, warmup, seq_len=4096):
     q, kp, vp = q.cuda(), kp.cuda(), vp.cuda()
     bt = wl.table_tensor(tables).cuda()
     lens = torch.tensor([seq_len], dtype=torch.int32, device="cuda")
-    ms = _time_gpu(lambda i=0: fa2_paged(q, kp, vp, bt, lens, max_kv_len=seq_len, is_causal=True),
-                   steps, warmup)
-    return ms, wl.causal_prefill_flops([seq_len])
+    ms, clock = _time_gpu(
+        lambda i=0: fa2_paged(q, kp, vp, bt, lens, max_kv_len=seq_len, is_causal=True), steps, warmup)
+    return ms, wl.causal_prefill_flops([seq_len]), clock
 
 
 def bench_decode(steps, warmup, rotate_bytes=2 << 30):
@@ -166,8 +173,8 @@ def bench_decode(steps, warmup, rotate_bytes=2 << 30):
         kpc, vpc = pools[i % copies]
         return fa2_paged(q, kpc, vpc, bt, lens_t, max_kv_len=max_kv)
 
-    ms = _time_gpu(step, steps, warmup)
-    return ms, wl.decode_bytes(lens), lens, copies
+    ms, clock = _time_gpu(step, steps, warmup)
+    return ms, wl.decode_bytes(lens), lens, copies, clock
 
 
 def bench_e2e(n_chats=16, reply_tokens=64, lo=32, hi=1000, seed=0, decode_graphs=True):
@@ -224,7 +231,9 @@ def e2e_line(e2e):
     def figs(r):
         return {"tok_per_s": round(r["tok_per_s"], 1), "wall_s": round(r["wall_s"], 3),
                 "ttft_p50_s": round(r["ttft_p50"], 4), "ttft_p99_s": round(r["ttft_p99"], 4),
-                "tpot_s": round(r["tpot"], 5)}
+                "lat_p50_s": round(r["lat_p50"], 4), "lat_p99_s": round(r["lat_p99"], 4),
+                "tpot_s": round(r["tpot"], 5), "peak_active": r["peak_active"],
+                "kv_util_pct": round(r["kv_util"], 1)}
     rec = {"metric": "e2e tok/s at 16 chats", "value": round(m["tok_per_s"], 1), "unit": "tok/s",
            "tokens": m["tokens"], "schedule": "mixed prefill+decode steps, decode-only steps "
            "replayed as HIP graphs, tokens drawn by the fused HIP sampler"}
@@ -284,11 +293,12 @@ def bench_plumbing(steps, warmup, seq_len=512, cpu_runs=21, cpu=True):
     q, k, v = wl.prefill_single(seq_len, dtype=torch.float32, seed=0)
     flops = wl.causal_prefill_flops([seq_len])
     qf, kf, vf = (t.cuda() for t in (q, k, v))
-    ms = _time_gpu(lambda i=0: FlashAttention2Function.apply(qf, kf, vf, True, None), steps, warmup)
+    ms, clock = _time_gpu(lambda i=0: FlashAttention2Function.apply(qf, kf, vf, True, None), steps,
+                          warmup)
     qb, kb, vb = (t.bfloat16() for t in (qf, kf, vf))
-    ms16 = _time_gpu(lambda i=0: FlashAttention2Function.apply(qb, kb, vb, True, None), steps,
-                     warmup)
-    out = {"gpu_ms": ms, "gpu_ms_bf16": ms16, "flops": flops}
+    ms16, clock16 = _time_gpu(lambda i=0: FlashAttention2Function.apply(qb, kb, vb, True, None),
+                              steps, warmup)
+    out = {"gpu_ms": ms, "gpu_ms_bf16": ms16, "flops": flops, "clock": clock, "clock_bf16": clock16}
     if cpu:
         sec = _median_time(lambda: sdpa_fallback(q, k, v, [0], 6), cpu_runs)
         out.update(cpu_sec=sec, cpu_threads=torch.get_num_threads())
@@ -321,8 +331,8 @@ def bench_copy(steps, warmup, nbytes=1 << 30):
     import torch
     src = torch.ones(nbytes // 2, dtype=torch.bfloat16, device="cuda")
     dst = torch.empty_like(src)
-    ms = _time_gpu(lambda i=0: dst.copy_(src), steps, warmup)
-    return ms, nbytes
+    ms, clock = _time_gpu(lambda i=0: dst.copy_(src), steps, warmup)
+    return ms, nbytes, clock
 
 
 def run_only(which, steps, warmup):
@@ -331,36 +341,63 @@ def run_only(which, steps, warmup):
         print(json.dumps(e2e_line(bench_e2e())), flush=True)
         return
     if which == "prefill":
-        ms, flops = bench_prefill(steps, warmup)
+        ms, flops, clock = bench_prefill(steps, warmup)
         rate, unit = flops / (ms * 1e-3) / 1e12, "TFLOP/s"
     elif which == "decode":
-        ms, nbytes, _, _ = bench_decode(steps, warmup)
+        ms, nbytes, _, _, clock = bench_decode(steps, warmup)
         rate, unit = nbytes / (ms * 1e-3) / 1e9, "GB/s"
     elif which == "paged":
-        ms, flops = bench_paged_prefill(steps, warmup)
+        ms, flops, clock = bench_paged_prefill(steps, warmup)
         rate, unit = flops / (ms * 1e-3) / 1e12, "TFLOP/s"
     elif which == "ragged":
-        ms, flops, _ = bench_ragged(steps, warmup)
+        ms, flops, _, clock = bench_ragged(steps, warmup)
         rate, unit = flops / (ms * 1e-3) / 1e12, "TFLOP/s"
     elif which == "plumbing":
         pl = bench_plumbing(steps, warmup, cpu=False)
         ms, rate, unit = pl["gpu_ms"], pl["flops"] / (pl["gpu_ms"] * 1e-3) / 1e12, "TFLOP/s"
+        clock = pl["clock"]
     else:
-        ms, nbytes = bench_copy(steps, warmup)
+        ms, nbytes, clock = bench_copy(steps, warmup)
         rate, unit = 2 * nbytes / (ms * 1e-3) / 1e9, "GB/s"
     print(json.dumps({"only": which, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 5),
-                      "value": round(rate, 2), "unit": unit}), flush=True)
+                      "value": round(rate, 2), "unit": unit, "clock": clock,
+                      "step_cycles": _cycles(ms, clock)}), flush=True)
+
+
+def _traffic_file():
+    path = ROOT / "profiles" / "traffic.json"
+    try:
+        return json.loads(path.read_text())
+    except (OSError, ValueError):
+        return {}
 
 
 def read_traffic(name):
-    """HBM bytes per launch recorded by the rocprofv3 --pmc summaries under profiles/, if any."""
-    path = ROOT / "profiles" / "traffic.json"
-    if not path.exists():
-        return None
-    try:
-        return json.loads(path.read_text()).get(name)
-    except (OSError, ValueError):
-        return None
+    """HBM bytes per launch recorded by the rocprofv3 --pmc summaries under profiles/, if any.
+    A static record of that profiling session (named by `traffic_session`), not a measurement of
+    this run."""
+    return _traffic_file().get(name)
+
+
+def traffic_session():
+    return _traffic_file().get("session")
+
+
+def _cycles(ms, clock):
+    """Shader cycles of one step at the clock the timed steps ran at."""
+    return round(ms * 1e-3 * clock["ghz"] * 1e9) if clock else None
+
+
+def _roofline(bound, achieved, peak, unit, clock, ms, traffic_key=None):
+    r = {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+         "frac": round(achieved / peak, 4)}
+    if traffic_key is not None:
+        r["traffic"] = read_traffic(traffic_key)
+        r["traffic_session"] = traffic_session()
+    r["clock_ghz"] = clock["ghz"] if clock else None
+    r["clock_xcd_range_ghz"] = [clock["min"], clock["max"]] if clock else None
+    r["step_cycles"] = _cycles(ms, clock)
+    return r
 
 
 def main():
@@ -391,7 +428,7 @@ def main():
         run_only(args.only, args.steps, args.warmup)
         return
 
-    ms, flops, cold_ms = bench_prefill(args.steps, args.warmup, cold=True)
+    ms, flops, clock, cold_ms = bench_prefill(args.steps, args.warmup, cold=True)
     tflops = flops / (ms * 1e-3) / 1e12
     out = {
         "metric": METRIC,
@@ -414,9 +451,8 @@ def main():
                        "value": round(flops / (cold_ms * 1e-3) / 1e12, 2),
                        "note": "the same warmup + steps timed right after the input upload, before "
                                "the untimed sustained-clock ramp that precedes every timed workload"},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": read_traffic("fa2_prefill_kernel")},
+        "roofline": _roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s", clock, ms,
+                              "fa2_prefill_kernel"),
     }
     if not args.no_cpu:
         cpu_tflops, cores, sec = cpu_prefill_baseline()
@@ -426,16 +462,15 @@ def main():
                                          f"SDPA oracle, median of 5 runs ({sec:.3f} s each)",
                                "host_cpu_count": os.cpu_count()}
     if not args.no_secondary:
-        dms, dbytes, lens, copies = bench_decode(args.steps, args.warmup)
+        dms, dbytes, lens, copies, dclock = bench_decode(args.steps, args.warmup)
         gbs = dbytes / (dms * 1e-3) / 1e9
         dec = {"metric": "paged-decode attn HBM GB/s", "value": round(gbs, 1), "unit": "GB/s",
                "ms_per_step": round(dms, 5), "bytes_per_step": dbytes,
                "workload": f"paged decode, 64 rows x 12q/2kv x head_dim 128, kv_len U[128,8192] "
                            f"(sum {sum(lens)}), 16-token blocks, permuted block table, bf16; "
                            f"{copies} pool copies rotated so no step hits the MALL",
-               "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                            "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                            "traffic": read_traffic("fa2_decode_kernel")}}
+               "roofline": _roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s", dclock, dms,
+                                     "fa2_decode_kernel")}
         if not args.no_cpu:
             cgbs, cores, sec = cpu_decode_baseline()
             dec["cpu_baseline"] = {"value": round(cgbs, 3), "unit": "GB/s", "cores": cores,
@@ -443,15 +478,14 @@ def main():
                                    "sample": f"16 of the 64 rows (their bytes over their time): "
                                              f"dense gather (kv_cache.py:117-121) + fp32 SDPA, "
                                              f"median of 5 runs ({sec:.3f} s each)"}
-        rms, rflops, rlens = bench_ragged(args.steps, args.warmup)
+        rms, rflops, rlens, rclock = bench_ragged(args.steps, args.warmup)
         rt = rflops / (rms * 1e-3) / 1e12
         rag = {"metric": "ragged varlen prefill attn TFLOP/s", "value": round(rt, 2),
                "unit": "TFLOP/s", "ms_per_step": round(rms, 5), "flops_per_step": rflops,
                "workload": f"16 packed causal sequences, L ~ U[16,1024] (sum {sum(rlens)}), "
                            f"12q/2kv, head_dim 128, bf16",
-               "roofline": {"bound": "mfma", "achieved": round(rt, 2), "peak": PEAK_BF16_TFLOPS,
-                            "unit": "TFLOP/s", "frac": round(rt / PEAK_BF16_TFLOPS, 4),
-                            "traffic": read_traffic("fa2_prefill_kernel_varlen")}}
+               "roofline": _roofline("mfma", rt, PEAK_BF16_TFLOPS, "TFLOP/s", rclock, rms,
+                                     "fa2_prefill_kernel_varlen")}
         if not args.no_cpu:
             ct, cores, sec = cpu_ragged_baseline()
             rag["cpu_baseline"] = {"value": round(ct, 4), "unit": "TFLOP/s", "cores": cores,
@@ -459,15 +493,14 @@ def main():
                                    "sample": f"the same 16 packed sequences in fp32, SDPA row by "
                                              f"row with each row's bottom-right mask, median of 7 "
                                              f"runs ({sec:.4f} s each)"}
-        pms, pflops = bench_paged_prefill(args.steps, args.warmup)
+        pms, pflops, pclock = bench_paged_prefill(args.steps, args.warmup)
         pt = pflops / (pms * 1e-3) / 1e12
         pag = {"metric": "paged prefill attn TFLOP/s", "value": round(pt, 2), "unit": "TFLOP/s",
                "ms_per_step": round(pms, 5), "flops_per_step": pflops,
                "workload": "causal prefill, 1 x 12q/2kv x 4096 x 128 bf16, K/V read from the paged "
                            "pool through a permuted table of 16-token blocks",
-               "roofline": {"bound": "mfma", "achieved": round(pt, 2), "peak": PEAK_BF16_TFLOPS,
-                            "unit": "TFLOP/s", "frac": round(pt / PEAK_BF16_TFLOPS, 4),
-                            "traffic": read_traffic("fa2_prefill_kernel_paged")}}
+               "roofline": _roofline("mfma", pt, PEAK_BF16_TFLOPS, "TFLOP/s", pclock, pms,
+                                     "fa2_prefill_kernel_paged")}
         pl = bench_plumbing(args.steps, args.warmup, cpu=not args.no_cpu)
         gt = pl["flops"] / (pl["gpu_ms"] * 1e-3) / 1e12
         gt16 = pl["flops"] / (pl["gpu_ms_bf16"] * 1e-3) / 1e12
@@ -476,11 +509,13 @@ def main():
                "dtype": "f32",
                "workload": "causal prefill 1 x 12q/2kv x 512 x 128, fp32 N(0,1) seed 0, through "
                            "FlashAttention2Function.apply in fp32 (the general kernel)",
-               "roofline": {"bound": "mfma", "achieved": round(gt, 2), "peak": PEAK_FP32_TFLOPS,
-                            "unit": "TFLOP/s", "frac": round(gt / PEAK_FP32_TFLOPS, 4)},
+               "roofline": _roofline("mfma", gt, PEAK_FP32_TFLOPS, "TFLOP/s", pl["clock"],
+                                     pl["gpu_ms"]),
                "bf16_cast": {"value": round(gt16, 2), "unit": "TFLOP/s",
                              "ms_per_step": round(pl["gpu_ms_bf16"], 5),
-                             "frac_of_bf16_peak": round(gt16 / PEAK_BF16_TFLOPS, 4)}}
+                             "frac_of_bf16_peak": round(gt16 / PEAK_BF16_TFLOPS, 4),
+                             "clock_ghz": pl["clock_bf16"]["ghz"] if pl["clock_bf16"] else None,
+                             "step_cycles": _cycles(pl["gpu_ms_bf16"], pl["clock_bf16"])}}
         if "cpu_sec" in pl:
             plb["cpu_baseline"] = {
                 "value": round(pl["flops"] / pl["cpu_sec"] / 1e12, 4), "unit": "TFLOP/s",

@@ -65,6 +65,42 @@ MI_FA2_API const char* mi_fa2_version(void);
 MI_FA2_API const char* mi_fa2_last_error(void);
 
 /*
+ * How the launches are sized for a device: no counterpart in the reference, whose Triton launcher
+ * sizes its grid from the shapes alone (kernels/fa2.py:192) and leaves the rest to the autotuner.
+ * The kernels size their grids from the device's compute units and deal work-groups over its XCDs
+ * (each XCD has its own L2); MI355X has 256 CUs in 8 XCDs, a partitioned device reports its own
+ * share.  num_cus <= 0: the plan of the current device (read once per device); otherwise the plan
+ * the library would use on a device of num_cus CUs in num_xcds XCDs (no GPU needed).
+ *   xcds_mapped: XCDs the prefill grid deals work-groups over (num_xcds if a power of two, else 1)
+ *   decode_work_groups_*: split-decode work-groups per launch (3 or 2 per CU; MI_FA2_DECODE_WGS
+ *   overrides both), capped at run time by the launch's 128-key chunk count.
+ */
+typedef struct mi_fa2_plan {
+  int32_t num_cus;
+  int32_t num_xcds;
+  int32_t xcds_mapped;
+  int32_t decode_work_groups_paged;
+  int32_t decode_work_groups_dense;
+} mi_fa2_plan;
+MI_FA2_API int mi_fa2_launch_plan(int32_t num_cus, int32_t num_xcds, mi_fa2_plan* out);
+
+/*
+ * Measurement support, no counterpart in the reference (which publishes no kernel timings): reads
+ * the shader clock on `stream`.  Launches n_groups single-wave work-groups; work-group w reads its
+ * CU's shader-cycle counter (s_memtime) and the 100 MHz real-time counter (s_memrealtime), spins
+ * until the latter has advanced by spin_ticks (10 ns each), reads both again and writes
+ *   out[5w] = cycles0, out[5w+1] = ticks0, out[5w+2] = cycles1, out[5w+3] = ticks1,
+ *   out[5w+4] = its XCD id;
+ * its CU's clock is (cycles1 - cycles0) / (ticks1 - ticks0) x 100 MHz.  The shader-cycle count is
+ * per CU and stops while the CU is clock-gated, so readings of different work-groups are never
+ * differenced.  A reading right before and one right after a timed region on the same stream
+ * bracket the clock that region ran at.  out: device memory, 8-byte aligned, 5 x n_groups
+ * uint64 (n_groups 1..1024, spin_ticks 1..100000).
+ */
+MI_FA2_API int mi_fa2_clock_stamp(uint64_t* out, int32_t n_groups, int32_t spin_ticks,
+                                  mi_fa2_stream_t stream);
+
+/*
  * Padded forward.  Replaces FlashAttention2Function.forward (kernels/fa2.py:164-214) and the Triton
  * launch at kernels/fa2.py:192-207, same argument meaning:
  *   q [batch, heads_q, seqlen_q, 128], k/v [batch, heads_kv, seqlen_k, 128], o like q,
@@ -153,8 +189,7 @@ MI_FA2_API int mi_fa2_fwd_paged(int32_t dtype, const void* q, const void* k_pool
 /*
  * The paged forward without a workspace: for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, hosts that forbid hipMalloc).  It has no
- * counterpart in the reference, whose launcher allocates its outputs per call
- * (kernels/fa2.py:188-189).  Same arguments, kernels and results as mi_fa2_fwd_paged, minus
+ * counterpart in the reference.  Same arguments, kernels and results as mi_fa2_fwd_paged, minus
  * workspace / workspace_bytes: the split-decode partials live in a scratch array of 32 MiB
  * (33,554,432 bytes) that the library holds on every GPU it runs on until the process ends
  * (e.g. 64 rows x 12 query heads at max_kv_len 8,192 use 25.6 MB).  A call that needs more

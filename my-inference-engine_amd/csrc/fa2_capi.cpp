@@ -24,6 +24,7 @@ int sample_chunks(int vocab);
 hipError_t launch_step_meta(const StepMetaParams& p, hipStream_t stream);
 hipError_t launch_add_rmsnorm(const ModelOpParams& p, int dtype, hipStream_t stream);
 hipError_t launch_silu_mul(const ModelOpParams& p, int dtype, hipStream_t stream);
+hipError_t launch_clock_stamp(uint64_t* out, int n_groups, int spin_ticks, hipStream_t stream);
 }  // namespace mi_fa2
 
 using mi_fa2::FwdParams;
@@ -50,10 +51,78 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 // Decode work split: the kernel cuts every (row, kv head) item into 128-key chunks and gives each
 // of its work-groups an equal contiguous share of all the chunks (stream-K); an item cut by a share
 // boundary leaves one partial per work-group touching it.  Work-groups launched: as many as fit on
-// the 256 CUs of MI355X at once (4 waves each: 2 per CU for the dense walk at 2 waves per SIMD, 3
-// per CU for the paged walk at 3 waves per SIMD), never more than there are chunks.
-// MI_FA2_DECODE_WGS overrides it, for tuning sweeps.
+// the device's CUs at once (4 waves each: 2 per CU for the dense walk at 2 waves per SIMD, 3 per CU
+// for the paged walk at 3 waves per SIMD; 512 and 768 on the 256 CUs of MI355X), never more than
+// there are chunks.  MI_FA2_DECODE_WGS overrides it, for tuning sweeps.
 constexpr int kDecodeChunk = 128;
+
+// What the launches are sized from: the device's compute units and XCDs (each XCD has its own L2,
+// and work-group w of a launch runs on XCD w % XCDs).  MI355X: 256 CUs in 8 XCDs; a partitioned
+// device reports its own share.  The XCD mapping of the prefill grid needs a power of two; any
+// other count maps as if there were one XCD (correct, only the L2 affinity is lost).
+struct Plan {
+  int cus, xcds, xcd_log2, decode_wgs_paged, decode_wgs_dense;
+};
+
+int forced_decode_wgs() {
+  static const int forced = [] {
+    const char* env = std::getenv("MI_FA2_DECODE_WGS");
+    const int v = env ? std::atoi(env) : 0;
+    return v > 0 ? v : 0;
+  }();
+  return forced;
+}
+
+Plan make_plan(int cus, int xcds) {
+  Plan pl{};
+  pl.cus = std::max(1, cus);
+  pl.xcds = std::max(1, xcds);
+  pl.xcd_log2 = 0;
+  while ((2 << pl.xcd_log2) <= pl.xcds && pl.xcd_log2 < 6) ++pl.xcd_log2;
+  if ((1 << pl.xcd_log2) != pl.xcds) pl.xcd_log2 = 0;
+  const int forced = forced_decode_wgs();
+  pl.decode_wgs_paged = forced ? forced : 3 * pl.cus;
+  pl.decode_wgs_dense = forced ? forced : 2 * pl.cus;
+  return pl;
+}
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_plan_once[kMaxDevices];
+Plan g_plan[kMaxDevices];
+hipError_t g_plan_err[kMaxDevices];
+
+// The current device's plan, read once per device.
+int plan_of_current_device(Plan* out) {
+  int dev = -1;
+  const hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess)
+    return fail(MI_FA2_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "device %d: the device table holds %d devices", dev,
+                kMaxDevices);
+  std::call_once(g_plan_once[dev], [dev] {
+    int cus = 0, xcds = 0;
+    g_plan_err[dev] = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (g_plan_err[dev] == hipSuccess)
+      g_plan_err[dev] = hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, dev);
+    g_plan[dev] = make_plan(cus, xcds);
+  });
+  if (g_plan_err[dev] != hipSuccess)
+    return fail(MI_FA2_ERR_LAUNCH, "reading device %d's CU / XCD counts failed: %s", dev,
+                hipGetErrorString(g_plan_err[dev]));
+  *out = g_plan[dev];
+  return MI_FA2_OK;
+}
+
+// Fills the launch's device fields (CU count, XCD mapping) from the current device.
+int set_device(FwdParams& p, Plan* plan = nullptr) {
+  Plan pl;
+  if (int rc = plan_of_current_device(&pl)) return rc;
+  p.n_cus = pl.cus;
+  p.xcd_log2 = pl.xcd_log2;
+  if (plan) *plan = pl;
+  return MI_FA2_OK;
+}
 
 // The split decode kernel serves one query per row, up to 16 query heads per kv head (the N of its
 // 16x16 MFMA) and up to 8192 rows (its row prefix sum lives in LDS); anything else runs through
@@ -72,14 +141,20 @@ int check_decode_strides(const FwdParams& p) {
   return MI_FA2_OK;
 }
 
-int decode_work_groups(int64_t batch, int64_t heads_kv, int64_t max_kv, bool paged) {
-  static const int forced = [] {
-    const char* env = std::getenv("MI_FA2_DECODE_WGS");
-    const int v = env ? std::atoi(env) : 0;
-    return v > 0 ? v : 0;
-  }();
+// The prefill kernel loads up to 64 K/V rows through one buffer resource (32-bit byte extent
+// rows x 2 bytes x stride) and adds 32-row offsets of 32-bit bytes: token strides stay below 2^24.
+int check_prefill_strides(int64_t k_st, int64_t v_st) {
+  const int64_t lim = int64_t(1) << 24;  // 64 rows x 2 bytes x stride < 2^31
+  if (k_st < 0 || v_st < 0 || k_st >= lim || v_st >= lim)
+    return fail(MI_FA2_ERR_UNSUPPORTED, "k/v token strides %lld / %lld: at most 2^24 - 1 elements",
+                (long long)k_st, (long long)v_st);
+  return MI_FA2_OK;
+}
+
+int decode_work_groups(const Plan& pl, int64_t batch, int64_t heads_kv, int64_t max_kv,
+                       bool paged) {
   const int64_t chunks = batch * heads_kv * std::max<int64_t>(1, (max_kv + kDecodeChunk - 1) / kDecodeChunk);
-  const int64_t want = forced ? forced : (paged ? 768 : 512);
+  const int64_t want = paged ? pl.decode_wgs_paged : pl.decode_wgs_dense;
   return (int)std::max<int64_t>(1, std::min(want, chunks));
 }
 
@@ -171,7 +246,6 @@ void set_lse(FwdParams& p, float* lse, const int64_t* s, int n) {
 constexpr size_t kScratchBytes = 32u << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
-constexpr int kMaxDevices = 64;
 std::once_flag g_scratch_once[kMaxDevices];
 void* g_scratch_ptr[kMaxDevices];
 hipError_t g_scratch_err[kMaxDevices];
@@ -245,9 +319,10 @@ int fwd_paged(int32_t dtype, const void* q, const void* k_pool, const void* v_po
   p.causal = is_causal ? 1 : 0;
   p.scale_log2 = sm_scale * mi_fa2::kLog2e;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // Every argument is checked before the device is looked at (its CU / XCD counts size the grid).
+  Plan plan;
 
   if (uses_decode(seqlen_q, p.group, batch)) {
-    p.n_wg = decode_work_groups(batch, heads_kv, max_kv_len, true);
     p.max_splits = decode_splits(max_kv_len);
     const size_t need = decode_workspace(batch, heads_q, heads_kv, max_kv_len);
     if (need && use_scratch) {
@@ -265,8 +340,12 @@ int fwd_paged(int32_t dtype, const void* q, const void* k_pool, const void* v_po
       set_workspace(p, workspace);
     }
     if (int rc = check_decode_strides(p)) return rc;
+    if (int rc = set_device(p, &plan)) return rc;
+    p.n_wg = decode_work_groups(plan, batch, heads_kv, max_kv_len, true);
     return launched(mi_fa2::launch_decode(p, dtype, mi_fa2::kPaged, s));
   }
+  if (int rc = check_prefill_strides(p.k_st, p.v_st)) return rc;
+  if (int rc = set_device(p, &plan)) return rc;
   return launched(mi_fa2::launch_prefill(p, dtype, mi_fa2::kPaged, seqlen_q, s));
 }
 
@@ -277,6 +356,35 @@ extern "C" {
 const char* mi_fa2_version(void) { return "mi_fa2 0.1.0 gfx950"; }
 
 const char* mi_fa2_last_error(void) { return g_err; }
+
+int mi_fa2_launch_plan(int32_t num_cus, int32_t num_xcds, mi_fa2_plan* out) {
+  if (!out) return fail(MI_FA2_ERR_INVALID, "out is NULL");
+  Plan pl;
+  if (num_cus > 0) {
+    pl = make_plan(num_cus, num_xcds);
+  } else if (int rc = plan_of_current_device(&pl)) {
+    return rc;
+  }
+  out->num_cus = pl.cus;
+  out->num_xcds = pl.xcds;
+  out->xcds_mapped = 1 << pl.xcd_log2;
+  out->decode_work_groups_paged = pl.decode_wgs_paged;
+  out->decode_work_groups_dense = pl.decode_wgs_dense;
+  return ok();
+}
+
+int mi_fa2_clock_stamp(uint64_t* out, int32_t n_groups, int32_t spin_ticks,
+                       mi_fa2_stream_t stream) {
+  if (!out) return fail(MI_FA2_ERR_INVALID, "out is NULL");
+  if (n_groups <= 0 || n_groups > 1024)
+    return fail(MI_FA2_ERR_INVALID, "n_groups %d: 1 to 1024 work-groups", n_groups);
+  if (spin_ticks < 1 || spin_ticks > 100000)
+    return fail(MI_FA2_ERR_INVALID, "spin_ticks %d: 1 to 100000 (10 ns each)", spin_ticks);
+  if (reinterpret_cast<uintptr_t>(out) % 8)
+    return fail(MI_FA2_ERR_INVALID, "out is not 8-byte aligned");
+  return launched(mi_fa2::launch_clock_stamp(out, n_groups, spin_ticks,
+                                             reinterpret_cast<hipStream_t>(stream)));
+}
 
 size_t mi_fa2_fwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv,
                                  int32_t seqlen_q, int32_t seqlen_k, int32_t head_dim) {
@@ -328,9 +436,10 @@ int mi_fa2_fwd(int32_t dtype, const void* q, const void* k, const void* v, void*
   p.causal = is_causal ? 1 : 0;
   p.scale_log2 = sm_scale * mi_fa2::kLog2e;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // Every argument is checked before the device is looked at (its CU / XCD counts size the grid).
+  Plan plan;
 
   if (uses_decode(seqlen_q, p.group, batch)) {
-    p.n_wg = decode_work_groups(batch, heads_kv, seqlen_k, false);
     p.max_splits = decode_splits(seqlen_k);
     const size_t need = decode_workspace(batch, heads_q, heads_kv, seqlen_k);
     if (need) {
@@ -340,8 +449,12 @@ int mi_fa2_fwd(int32_t dtype, const void* q, const void* k, const void* v, void*
       set_workspace(p, workspace);
     }
     if (int rc = check_decode_strides(p)) return rc;
+    if (int rc = set_device(p, &plan)) return rc;
+    p.n_wg = decode_work_groups(plan, batch, heads_kv, seqlen_k, false);
     return launched(mi_fa2::launch_decode(p, dtype, mi_fa2::kDense, s));
   }
+  if (int rc = check_prefill_strides(p.k_st, p.v_st)) return rc;
+  if (int rc = set_device(p, &plan)) return rc;
   return launched(mi_fa2::launch_prefill(p, dtype, mi_fa2::kDense, seqlen_q, s));
 }
 
@@ -397,6 +510,7 @@ int mi_fa2_fwd_general(int32_t dtype, const void* q, const void* k, const void* 
   p.S = seqlen_k;
   p.causal = is_causal ? 1 : 0;
   p.scale_log2 = sm_scale * mi_fa2::kLog2e;
+  if (int rc = set_device(p)) return rc;
   return launched(mi_fa2::launch_general(p, dtype, head_dim, head_dim_v,
                                          reinterpret_cast<hipStream_t>(stream)));
 }
@@ -438,6 +552,8 @@ int mi_fa2_fwd_varlen(int32_t dtype, const void* q, const void* k, const void* v
   p.group = heads_q / heads_kv;
   p.causal = is_causal ? 1 : 0;
   p.scale_log2 = sm_scale * mi_fa2::kLog2e;
+  if (int rc = check_prefill_strides(p.k_st, p.v_st)) return rc;
+  if (int rc = set_device(p)) return rc;
   return launched(mi_fa2::launch_prefill(p, dtype, mi_fa2::kVarlen, max_seqlen_q,
                                          reinterpret_cast<hipStream_t>(stream)));
 }
@@ -526,6 +642,8 @@ int mi_fa2_fwd_paged_varlen(int32_t dtype, const void* q, const void* k_pool, co
   p.S = max_kv_len;
   p.causal = is_causal ? 1 : 0;
   p.scale_log2 = sm_scale * mi_fa2::kLog2e;
+  if (int rc = check_prefill_strides(p.k_st, p.v_st)) return rc;
+  if (int rc = set_device(p)) return rc;
   return launched(mi_fa2::launch_prefill(p, dtype, mi_fa2::kPagedVarlen, max_seqlen_q,
                                          reinterpret_cast<hipStream_t>(stream)));
 }

@@ -122,6 +122,10 @@ struct FwdParams {
   int32_t* ws_np;             // decode: partials per (row, kv head) item, [B][Hkv]
   int32_t n_wg;               // decode: work-groups launched
   int32_t max_splits;         // decode: partial slots per (row, query head)
+  // the device's compute units and log2 of its XCD count (each XCD has its own L2), read once per
+  // device by the C ABI: they size grids and map work-groups to XCDs
+  int32_t n_cus;
+  int32_t xcd_log2;
 };
 
 // Everything the fused RoPE + KV-write launch needs (rope_kv.hip).

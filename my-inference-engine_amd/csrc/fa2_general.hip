@@ -533,9 +533,10 @@ template <class E, int D, int DV>
 hipError_t launch_general_t(const FwdParams& p, hipStream_t stream) {
   const int rows_per_wg = kGenWaves * kGenRows;
   const int64_t tiles = (int64_t)((p.T + rows_per_wg - 1) / rows_per_wg) * p.Hq * p.B;
-  // Fewer query rows than a work-group holds, or fewer work-groups than MI355X's 256 CUs: split
-  // each 16-row tile's keys over 4 waves instead (4x the work-groups, a quarter of the chain).
-  if (p.T < rows_per_wg || tiles < 256) {
+  // Fewer query rows than a work-group holds, or fewer work-groups than the device's CUs (256 on
+  // MI355X): split each 16-row tile's keys over 4 waves instead (4x the work-groups, a quarter of
+  // the chain).
+  if (p.T < rows_per_wg || tiles < p.n_cus) {
     const dim3 grid((p.T + kGenRows - 1) / kGenRows, p.Hq, p.B);
     hipLaunchKernelGGL((fa2_general_split_kernel<E, D, DV>), grid, dim3(64 * kGenWaves), 0,
                        stream, p);

@@ -63,31 +63,32 @@ struct Parity {
   static constexpr int value = P;
 };
 
-// Work-groups are dispatched round-robin over the chip's 8 XCDs (work-group w runs on XCD w % 8),
-// and each XCD has its own L2.  The (row, query head, query tile) of work-group w is chosen so that
-// the query heads sharing one kv head (one class c = (row, kv head)) and tile run on the same XCD,
-// so one L2 holds their K/V, and so that every XCD walks its tiles longest first with the same
-// mix of tile lengths.  rank 0 is a row's last (longest) query tile.
-//   * classes dividing 8 (one or a few long rows): each class has 8 / classes XCDs of its own, and
+// Work-groups are dispatched round-robin over the device's X XCDs (work-group w runs on XCD w % X),
+// and each XCD has its own L2.  X is read from the device (8 on a whole MI355X, fewer on a
+// partitioned one; a power of two, passed as log2; with X = 1 every mapping below reduces to plain
+// rank-major order).  The (row, query head, query tile) of work-group w is chosen so that the
+// query heads sharing one kv head (one class c = (row, kv head)) and tile run on the same XCD, so
+// one L2 holds their K/V, and so that every XCD walks its tiles longest first with the same mix
+// of tile lengths.  rank 0 is a row's last (longest) query tile.
+//   * classes dividing X (one or a few long rows): each class has X / classes XCDs of its own, and
 //     every XCD walks its class's tiles rank by rank;
 //   * otherwise (batches of rows, of equal or ragged lengths): the groups (class, rank) are taken
 //     rank-major, group j = rank * stride + c with an odd stride >= classes, and dealt to XCD
-//     j % 8.  The odd stride rotates a class over the XCDs from one rank to the next, so rows of
+//     j % X.  The odd stride rotates a class over the XCDs from one rank to the next, so rows of
 //     different lengths spread over all XCDs instead of pinning a class -- and its row's whole
-//     work -- to XCD c % 8 (16 ragged rows of U[16, 1024] tokens: the busiest XCD carried 1.9x
-//     the least busy one's tiles that way).
+//     work -- to XCD c % X (16 ragged rows of U[16, 1024] tokens on 8 XCDs: the busiest XCD
+//     carried 1.9x the least busy one's tiles that way).
 //   * packed batches of at most 64 rows (the varlen modes) number only the real (class, rank)
-//     groups, rank-major, and deal group j to XCD j % 8 (prefill_item_packed): a row's class moves
+//     groups, rank-major, and deal group j to XCD j % X (prefill_item_packed): a row's class moves
 //     over the XCDs as shorter rows drop out of the later ranks.
-constexpr int kXcds = 8;
-
-__host__ __device__ inline int prefill_grid_size(int classes, int group, int n_qt) {
-  if (classes < kXcds && kXcds % classes == 0) {
-    const int per_xcd = (classes * group * n_qt + kXcds - 1) / kXcds;
-    return kXcds * per_xcd;
+inline int prefill_grid_size(int classes, int group, int n_qt, int xcd_log2) {
+  const int X = 1 << xcd_log2;
+  if (classes < X && X % classes == 0) {
+    const int per_xcd = (classes * group * n_qt + X - 1) / X;
+    return X * per_xcd;
   }
   const int stride = classes | 1;
-  return kXcds * ((stride * n_qt + kXcds - 1) / kXcds) * group;
+  return X * ((stride * n_qt + X - 1) / X) * group;
 }
 
 // Division by a divisor fixed for the launch, as a multiply: n / d = umulhi(n, m) >> l with
@@ -109,17 +110,19 @@ __device__ __forceinline__ int fdiv(int n, const FastDiv& f) {
   return (int)(f.m ? __umulhi((uint32_t)n, f.m) >> f.l : (uint32_t)n >> f.l);
 }
 
-// The launch's item map: the divisors of prefill_item and, when the classes divide the XCDs,
-// log2 of the XCDs per class (else -1).
+// The launch's item map: the divisors of prefill_item, log2 of the device's XCD count and, when
+// the classes divide the XCDs, log2 of the XCDs per class (else -1).
 struct ItemMap {
   FastDiv group, stride, hkv;
-  int32_t classes, xcd_shift;
+  int32_t classes, xcd_shift, xcd_log2;
 };
-inline ItemMap make_item_map(int classes, int group, int Hkv) {
-  ItemMap m{make_fastdiv(group), make_fastdiv(classes | 1), make_fastdiv(Hkv), classes, -1};
-  if (classes < kXcds && kXcds % classes == 0) {
+inline ItemMap make_item_map(int classes, int group, int Hkv, int xcd_log2) {
+  ItemMap m{make_fastdiv(group), make_fastdiv(classes | 1), make_fastdiv(Hkv), classes, -1,
+            xcd_log2};
+  const int X = 1 << xcd_log2;
+  if (classes < X && X % classes == 0) {
     m.xcd_shift = 0;
-    while ((classes << m.xcd_shift) < kXcds) ++m.xcd_shift;
+    while ((classes << m.xcd_shift) < X) ++m.xcd_shift;
   }
   return m;
 }
@@ -127,7 +130,7 @@ inline ItemMap make_item_map(int classes, int group, int Hkv) {
 // Returns false for the padding work-groups of the grid.
 __device__ inline bool prefill_item(int w, const ItemMap& map, int n_qt, int& b, int& h,
                                     int& rank) {
-  const int x = w % kXcds, slot = w / kXcds;
+  const int x = w & ((1 << map.xcd_log2) - 1), slot = w >> map.xcd_log2;
   const int group = (int)map.group.d;
   int c;
   if (map.xcd_shift >= 0) {
@@ -139,7 +142,7 @@ __device__ inline bool prefill_item(int w, const ItemMap& map, int n_qt, int& b,
   } else {
     const int stride = (int)map.stride.d;
     const int sg = fdiv(slot, map.group);
-    const int j = sg * kXcds + x;  // group, rank-major
+    const int j = (sg << map.xcd_log2) + x;  // group, rank-major
     rank = fdiv(j, map.stride);
     c = j - rank * stride;
     if (c >= map.classes) return false;
@@ -165,10 +168,10 @@ __device__ inline bool prefill_item_packed(const FwdParams& p, int w, const Item
     const int t = p.cu_q[lane + 1] - p.cu_q[lane];
     nq = t > 0 ? (t + kPfRows - 1) / kPfRows : 0;
   }
-  const int x = w % kXcds, slot = w / kXcds;
+  const int x = w & ((1 << map.xcd_log2) - 1), slot = w >> map.xcd_log2;
   const int sg = fdiv(slot, map.group);
   const int hkv = (int)map.hkv.d;
-  int j = sg * kXcds + x;  // the j-th real group (rank, class), rank-major
+  int j = (sg << map.xcd_log2) + x;  // the j-th real group (rank, class), rank-major
   int r = 0;
   uint64_t rows = 0;
   for (; r < n_qt; ++r) {
@@ -793,10 +796,11 @@ static hipError_t launch_prefill_t(const FwdParams& p, int max_seqlen_q, hipStre
   // Packed batches: one slot per (rank, class, query head) of the full B x n_qt box, numbered by
   // prefill_item_packed (real tiles first).
   const bool packed = (MODE == kVarlen || MODE == kPagedVarlen) && p.B <= 64;
-  const int grid = packed ? kXcds * p.group * ((p.B * p.Hkv * n_qt + kXcds - 1) / kXcds)
-                          : prefill_grid_size(p.B * p.Hkv, p.group, n_qt);
+  const int X = 1 << p.xcd_log2;
+  const int grid = packed ? X * p.group * ((p.B * p.Hkv * n_qt + X - 1) / X)
+                          : prefill_grid_size(p.B * p.Hkv, p.group, n_qt, p.xcd_log2);
   hipLaunchKernelGGL((fa2_prefill_kernel<E, MODE>), dim3(grid), dim3(kPfThreads), 0, stream, p,
-                     n_qt, make_item_map(p.B * p.Hkv, p.group, p.Hkv));
+                     n_qt, make_item_map(p.B * p.Hkv, p.group, p.Hkv, p.xcd_log2));
   return hipGetLastError();
 }
 

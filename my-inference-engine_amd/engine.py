@@ -142,7 +142,8 @@ class Engine:
                     break
         self._process()
 
-    def run_until_idle(self, max_ticks=1_000_000):
+    def run_until_idle(self, max_ticks=1_000_000, on_tick=None):
+        """Tick until nothing is queued, deferred or active; on_tick() runs after every tick."""
         for _ in range(max_ticks):
             if self.idle():
                 return
@@ -151,6 +152,8 @@ class Engine:
                 raise RuntimeError("deferred jobs can never be admitted: nothing else will "
                                    "release cache blocks")
             self.tick()
+            if on_tick is not None:
+                on_tick()
         raise RuntimeError("scheduler did not drain")
 
     def _fits_after_eviction(self, job):
@@ -294,11 +297,21 @@ def run_concurrent_chats(engine, prompts, reply_tokens):
 
     Returns the reference benchmark's summary (metrics/benchmark_concurrency.py:57-76): generated
     tokens / wall time from the first submit to the last finish, TTFT / latency percentiles,
-    time per output token."""
+    time per output token, the peak number of active (decoding) chats and the KV utilisation:
+    the peak token count held by the chats' conversations as a percentage of the cache's token
+    capacity (metrics/benchmark_concurrency.py:151-159,176, where the reference samples both
+    from a thread every few milliseconds; here they are sampled after every scheduler tick, from
+    host-side state only)."""
     convs = [Conversation() for _ in prompts]
+    peak = {"active": 0, "cached": 0}
+
+    def sample():
+        peak["active"] = max(peak["active"], len(engine.active))
+        peak["cached"] = max(peak["cached"], sum(len(c.ids) for c in convs if c.seq is not None))
+
     start = time.perf_counter()
     jobs = [engine.submit(c, p, reply_tokens) for c, p in zip(convs, prompts)]
-    engine.run_until_idle()
+    engine.run_until_idle(on_tick=sample)
     torch.cuda.synchronize() if engine.device.type == "cuda" else None
     wall = time.perf_counter() - start
     for c in convs:
@@ -314,6 +327,8 @@ def run_concurrent_chats(engine, prompts, reply_tokens):
     ttft = [j.t_first - j.t_submit for j in jobs]
     lat = [j.t_done - j.t_submit for j in jobs]
     tpot = [(j.t_done - j.t_first) / (len(j.generated) - 1) for j in jobs if len(j.generated) > 1]
+    capacity = engine.cache.num_blocks * engine.cache.block_size
     return {"chats": len(prompts), "tokens": tokens, "wall_s": wall, "tok_per_s": tokens / wall,
             "ttft_p50": pct(ttft, 50), "ttft_p99": pct(ttft, 99), "lat_p50": pct(lat, 50),
-            "lat_p99": pct(lat, 99), "tpot": sum(tpot) / max(1, len(tpot))}
+            "lat_p99": pct(lat, 99), "tpot": sum(tpot) / max(1, len(tpot)),
+            "peak_active": peak["active"], "kv_util": 100.0 * peak["cached"] / capacity}

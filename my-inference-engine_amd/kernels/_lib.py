@@ -24,10 +24,20 @@ _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
 _sz = ctypes.c_size_t
 
+
+class Plan(ctypes.Structure):
+    """mi_fa2_plan: how the launches are sized for a device (its CUs and XCDs)."""
+    _fields_ = [("num_cus", ctypes.c_int32), ("num_xcds", ctypes.c_int32),
+                ("xcds_mapped", ctypes.c_int32), ("decode_work_groups_paged", ctypes.c_int32),
+                ("decode_work_groups_dense", ctypes.c_int32)]
+
+
 # name -> (restype, argtypes); mirrors include/mi_fa2.h
 SIGNATURES = {
     "mi_fa2_version": (ctypes.c_char_p, []),
     "mi_fa2_last_error": (ctypes.c_char_p, []),
+    "mi_fa2_launch_plan": (_i32, [_i32, _i32, ctypes.POINTER(Plan)]),
+    "mi_fa2_clock_stamp": (_i32, [_p, _i32, _i32, _p]),
     "mi_fa2_fwd_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "mi_fa2_fwd": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
                           _p, _p, _p, _p, _p, _i32, _f32, _p, _sz, _p]),
@@ -98,3 +108,37 @@ def strides(t, n=None):
 
 def stream_of(t):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def device_index(dev):
+    """The index of a cuda device ("cuda" alone: the current one)."""
+    return dev.index if dev.index is not None else torch._C._cuda_getDevice()
+
+
+class on_device:
+    """`with on_device(dev) as stream:` makes dev the current device for the block (only if it is
+    not already: the common case costs two integer reads) and yields the raw handle of dev's
+    current stream, the stream a launch goes to."""
+    __slots__ = ("idx", "prev")
+
+    def __init__(self, dev):
+        self.idx = device_index(dev)
+
+    def __enter__(self):
+        self.prev = torch._C._cuda_getDevice()
+        if self.prev != self.idx:
+            torch._C._cuda_setDevice(self.idx)
+        return torch._C._cuda_getCurrentRawStream(self.idx)
+
+    def __exit__(self, *exc):
+        if self.prev != self.idx:
+            torch._C._cuda_setDevice(self.prev)
+        return False
+
+
+def launch_plan(num_cus=0, num_xcds=0):
+    """The launch plan for a device of num_cus CUs in num_xcds XCDs, or (num_cus <= 0) for the
+    current device."""
+    pl = Plan()
+    check(load().mi_fa2_launch_plan(num_cus, num_xcds, ctypes.byref(pl)))
+    return {name: getattr(pl, name) for name, _ in Plan._fields_}

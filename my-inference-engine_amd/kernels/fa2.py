@@ -36,9 +36,26 @@ from . import _lib
 HEAD_DIM = 128
 
 
+_MEMO_MAX = 4096
+_STRIDES_OK = {}
+_STRIDE_ARRAYS = {}
+
+
+def _strides_ok(t):
+    """Strides that allow 16-byte vector loads (the base alignment is checked per call)."""
+    key = (t.shape, t.stride())
+    ok = _STRIDES_OK.get(key)
+    if ok is None:
+        shape, stride = key
+        ok = stride[-1] == 1 and all(st % 8 == 0 for st, n in zip(stride[:-1], shape[:-1]) if n > 1)
+        if len(_STRIDES_OK) >= _MEMO_MAX:
+            _STRIDES_OK.clear()
+        _STRIDES_OK[key] = ok
+    return ok
+
+
 def _dims_ok(t):
-    return t.data_ptr() % 16 == 0 and t.stride(-1) == 1 and all(
-        st % 8 == 0 for st, n in zip(t.stride()[:-1], t.shape[:-1]) if n > 1)
+    return t.data_ptr() % 16 == 0 and _strides_ok(t)
 
 
 def _vec(t):
@@ -46,16 +63,47 @@ def _vec(t):
     return t if _dims_ok(t) else t.contiguous()
 
 
-def _strides(t):
+def _contig(shape):
+    return tuple(math.prod(shape[i + 1:]) for i in range(len(shape)))
+
+
+def _strides_of(shape, stride):
     # A size-1 dimension is only ever indexed at 0, so its stride never moves an address, and torch
     # may report any value there (0 after expand, anything after a view).  The kernels also use a
     # token stride as the row pitch of their load extents (a load of `rows` rows reads at most
     # rows * stride elements from the first row's start), so a size-1 dimension gets the stride it
     # would have in a contiguous tensor: the product of the sizes after it, never less than the
     # head dim.  (A 0 there made a single-token K or V read as zeros.)
-    s = [math.prod(t.shape[i + 1:]) if n == 1 else st
-         for i, (st, n) in enumerate(zip(t.stride(), t.shape))]
-    return (_lib.ctypes.c_int64 * len(s))(*s)
+    # The arrays are memoised by (shape, stride): the C ABI only reads them.
+    key = (tuple(shape), tuple(stride))
+    arr = _STRIDE_ARRAYS.get(key)
+    if arr is None:
+        s = [math.prod(shape[i + 1:]) if n == 1 else st
+             for i, (st, n) in enumerate(zip(stride, shape))]
+        arr = (_lib.ctypes.c_int64 * len(s))(*s)
+        if len(_STRIDE_ARRAYS) >= _MEMO_MAX:
+            _STRIDE_ARRAYS.clear()
+        _STRIDE_ARRAYS[key] = arr
+    return arr
+
+
+def _strides(t):
+    return _strides_of(t.shape, t.stride())
+
+
+_POOL_STRIDES = {}
+
+
+def _pool_strides(pool):
+    """(slot, head) strides of a [slots, Hkv, d] pool, as they are."""
+    key = pool.stride()[:2]
+    arr = _POOL_STRIDES.get(key)
+    if arr is None:
+        arr = (_lib.ctypes.c_int64 * 2)(*key)
+        if len(_POOL_STRIDES) >= _MEMO_MAX:
+            _POOL_STRIDES.clear()
+        _POOL_STRIDES[key] = arr
+    return arr
 
 
 GENERAL_DIMS = (16, 32, 64, 128, 256)
@@ -94,7 +142,7 @@ def _workspace(nbytes, device):
     address, and torch keeps alive only the memory a capture itself allocated."""
     if not nbytes:
         return None
-    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    key = (device, torch._C._cuda_getCurrentRawStream(_lib.device_index(device)))
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         size = int(nbytes)
@@ -108,62 +156,127 @@ def _workspace(nbytes, device):
     return ws
 
 
+class _Padded:
+    """The validated launch of one padded-call shape: its checks ran once, its constant arguments
+    (sizes, stride arrays, output shapes, which kernel) are built once, and every later call of the
+    same shapes, strides, dtypes, device and causality only allocates O and L and launches.
+
+    Checked per call, not cached: tensor base alignment (16 bytes) and kv_lens."""
+    __slots__ = ("fast", "dtype_code", "dev", "o_shape", "l_shape", "copy_q", "copy_k", "copy_v",
+                 "head", "tail", "ws_bytes")
+
+
+_PADDED = {}
+_MEMO_MAX = 4096
+
+
+def _plan_padded(Q, K, V, is_causal):
+    """Every check of FlashAttention2Function.forward (kernels/fa2.py:172-185), then the launch's
+    constant arguments."""
+    batch_size, num_heads, seq_len, d = Q.shape
+    seq_len_k = K.shape[2]
+    d_v = V.shape[-1]
+    sm_scale = 1.0 / math.sqrt(d)
+    assert Q.is_cuda and K.is_cuda and V.is_cuda, "Q, K and V must be GPU tensors"
+    num_kv_heads = K.shape[1]
+    assert Q.shape[0] == K.shape[0] and Q.shape[-1] == K.shape[-1], \
+        "Q and K must agree in batch size and head dim"
+    assert num_heads % num_kv_heads == 0, "query heads must be a multiple of kv heads (GQA)"
+    assert K.shape[:-1] == V.shape[:-1], "K and V may differ only in their last dimension"
+    assert (d & (d - 1) == 0) and (d_v & (d_v - 1) == 0), "d and d_v must be powers of 2"
+    fast = Q.dtype in _lib.DTYPES and d == HEAD_DIM and d_v == HEAD_DIM
+    if fast:
+        _envelope(Q, K, V)
+    else:
+        _general_envelope(Q, K, V)
+    pl = _Padded()
+    pl.fast = fast
+    pl.dtype_code = (_lib.DTYPES if fast else _lib.GENERAL_DTYPES)[Q.dtype]
+    pl.dev = Q.device
+    pl.o_shape = (batch_size, num_heads, seq_len, d_v)
+    pl.l_shape = (batch_size, num_heads, seq_len)
+    # a tensor whose strides do not allow 16-byte vector loads goes through a contiguous copy
+    pl.copy_q, pl.copy_k, pl.copy_v = (not _strides_ok(t) for t in (Q, K, V))
+    lay = lambda t, cp: _strides_of(t.shape, _contig(t.shape) if cp else t.stride())  # noqa: E731
+    o_st = _strides_of(pl.o_shape, _contig(pl.o_shape))
+    l_st = _strides_of(pl.l_shape, _contig(pl.l_shape))
+    qs, ks, vs = lay(Q, pl.copy_q), lay(K, pl.copy_k), lay(V, pl.copy_v)
+    if fast:
+        pl.head = (batch_size, num_heads, num_kv_heads, seq_len, seq_len_k, d)
+        pl.tail = (qs, ks, vs, o_st, l_st, int(bool(is_causal)), sm_scale)
+        pl.ws_bytes = _lib.load().mi_fa2_fwd_workspace_size(batch_size, num_heads, num_kv_heads,
+                                                             seq_len, seq_len_k, d)
+    else:
+        pl.head = (batch_size, num_heads, num_kv_heads, seq_len, seq_len_k, d, d_v)
+        pl.tail = (qs, ks, vs, o_st, l_st, int(bool(is_causal)), sm_scale)
+        pl.ws_bytes = 0
+    return pl
+
+
+def _run_padded(Q, K, V, is_causal, kv_lens):
+    """The padded forward: (O, L), launched on the current stream of Q's device."""
+    key = (Q.shape, Q.stride(), K.shape, K.stride(), V.shape, V.stride(), Q.dtype, K.dtype,
+           V.dtype, Q.device, K.device, V.device, bool(is_causal))
+    pl = _PADDED.get(key)
+    if pl is None:
+        pl = _plan_padded(Q, K, V, is_causal)
+        if len(_PADDED) >= _MEMO_MAX:
+            _PADDED.clear()
+        _PADDED[key] = pl
+    if kv_lens is not None:
+        assert kv_lens.shape == (pl.o_shape[0],) and kv_lens.dtype == torch.int32, \
+            "kv_lens must be an int32 tensor of shape [batch]"
+        assert kv_lens.device == Q.device, "kv_lens must be on Q's device"
+    q = Q.contiguous() if pl.copy_q else Q
+    k = K.contiguous() if pl.copy_k else K
+    v = V.contiguous() if pl.copy_v else V
+    tail = pl.tail
+    if (q.data_ptr() | k.data_ptr() | v.data_ptr()) & 15:
+        # a view starting off a 16-byte boundary: an aligned copy (.contiguous() would return an
+        # already-contiguous view as it is), launched with the copies' own strides
+        q, k, v = (t.clone(memory_format=torch.contiguous_format) if t.data_ptr() & 15 else t
+                   for t in (q, k, v))
+        tail = (_strides(q), _strides(k), _strides(v)) + tail[3:]
+    dev = pl.dev
+    O = torch.empty(pl.o_shape, device=dev, dtype=Q.dtype)
+    L = torch.empty(pl.l_shape, device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    lens = kv_lens.data_ptr() if kv_lens is not None else None
+    with _lib.on_device(dev) as stream:
+        if pl.fast:
+            ws = _workspace(pl.ws_bytes, dev)
+            _lib.check(lib.mi_fa2_fwd(
+                pl.dtype_code, q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(),
+                L.data_ptr(), lens, *pl.head, *tail,
+                ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+                stream))
+        else:
+            _lib.check(lib.mi_fa2_fwd_general(
+                pl.dtype_code, q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(),
+                L.data_ptr(), lens, *pl.head, *tail, stream))
+    return O, L
+
+
 class FlashAttention2Function(torch.autograd.Function):
     @staticmethod
     def forward(ctx, Q, K, V, is_causal=False, kv_lens=None):
         # Q [B, Hq, T, d], K/V [B, Hkv, S, d]; kv_lens [B] int32: real keys per row (the rest of
         # K/V is padding); causal masking is aligned to each row's last key.
-        batch_size, num_heads, seq_len, d = Q.shape
-        seq_len_k = K.shape[2]
-        d_v = V.shape[-1]
-        sm_scale = 1.0 / math.sqrt(d)
-
-        assert Q.is_cuda and K.is_cuda and V.is_cuda, "Q, K and V must be GPU tensors"
-        num_kv_heads = K.shape[1]
-        assert Q.shape[0] == K.shape[0] and Q.shape[-1] == K.shape[-1], \
-            "Q and K must agree in batch size and head dim"
-        assert num_heads % num_kv_heads == 0, "query heads must be a multiple of kv heads (GQA)"
-        assert K.shape[:-1] == V.shape[:-1], "K and V may differ only in their last dimension"
-        if kv_lens is not None:
-            assert kv_lens.shape == (batch_size,) and kv_lens.dtype == torch.int32, \
-                "kv_lens must be an int32 tensor of shape [batch]"
-            assert kv_lens.device == Q.device, "kv_lens must be on Q's device"
-        assert (d & (d - 1) == 0) and (d_v & (d_v - 1) == 0), "d and d_v must be powers of 2"
-        fast = Q.dtype in _lib.DTYPES and d == HEAD_DIM and d_v == HEAD_DIM
-        if fast:
-            _envelope(Q, K, V)
-        else:
-            _general_envelope(Q, K, V)
-
-        O = torch.empty((batch_size, num_heads, seq_len, d_v), device=Q.device, dtype=Q.dtype)
-        L = torch.empty((batch_size, num_heads, seq_len), device=Q.device, dtype=torch.float32)
-        q, k, v = _vec(Q), _vec(K), _vec(V)
-        lib = _lib.load()
+        O, L = _run_padded(Q, K, V, is_causal, kv_lens)
         ctx.save_for_backward(Q, K, V, O, L)
         ctx.is_causal = is_causal
-        ctx.scale = sm_scale
-        if not fast:
-            with torch.cuda.device(Q.device):
-                _lib.check(lib.mi_fa2_fwd_general(
-                    _lib.GENERAL_DTYPES[Q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                    O.data_ptr(), L.data_ptr(),
-                    kv_lens.data_ptr() if kv_lens is not None else None,
-                    batch_size, num_heads, num_kv_heads, seq_len, seq_len_k, d, d_v,
-                    _strides(q), _strides(k), _strides(v), _strides(O), _strides(L),
-                    int(bool(is_causal)), sm_scale, _lib.stream_of(Q)))
-            return O
-        nbytes = lib.mi_fa2_fwd_workspace_size(batch_size, num_heads, num_kv_heads, seq_len,
-                                               seq_len_k, d)
-        ws = _workspace(nbytes, Q.device)
-        with torch.cuda.device(Q.device):
-            _lib.check(lib.mi_fa2_fwd(
-                _lib.DTYPES[Q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(),
-                L.data_ptr(), kv_lens.data_ptr() if kv_lens is not None else None,
-                batch_size, num_heads, num_kv_heads, seq_len, seq_len_k, d,
-                _strides(q), _strides(k), _strides(v), _strides(O), _strides(L),
-                int(bool(is_causal)), sm_scale,
-                ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _lib.stream_of(Q)))
+        ctx.scale = 1.0 / math.sqrt(Q.shape[-1])
         return O
+
+    @classmethod
+    def apply(cls, Q, K, V, is_causal=False, kv_lens=None):
+        """Same call and result as torch.autograd.Function.apply.  The reference's Function has a
+        forward only (kernels/fa2.py:164-214): an autograd node is recorded when an input
+        requires grad, as before; otherwise (inference, every call of the engine) the forward runs
+        directly, without the node machinery's host cost (several microseconds per call)."""
+        if torch.is_grad_enabled() and (Q.requires_grad or K.requires_grad or V.requires_grad):
+            return super().apply(Q, K, V, is_causal, kv_lens)
+        return _run_padded(Q, K, V, is_causal, kv_lens)[0]
 
 
 def fa2_forward(Q, K, V, is_causal=False, kv_lens=None, return_lse=False):
@@ -220,18 +333,30 @@ def fa2_paged(q, k_pool, v_pool, block_table, kv_lens, *, block_size=16, max_kv_
     assert O.shape == q.shape and O.dtype == q.dtype and _dims_ok(O)
     L = torch.empty((B, Hq, T), device=q.device, dtype=torch.float32)
     lib = _lib.load()
-    nbytes = lib.mi_fa2_fwd_paged_workspace_size(B, Hq, Hkv, T, max_kv_len, d)
-    ws = _workspace(nbytes, q.device)
-    pool_strides = (_lib.ctypes.c_int64 * 2)(*k_pool.stride()[:2])
-    with torch.cuda.device(q.device):
+    ws = _workspace(_paged_ws_bytes(B, Hq, Hkv, T, int(max_kv_len), d), q.device)
+    pool_strides = _pool_strides(k_pool)
+    with _lib.on_device(q.device) as stream:
         _lib.check(lib.mi_fa2_fwd_paged(
             _lib.DTYPES[q.dtype], q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), O.data_ptr(),
             L.data_ptr(), block_table.data_ptr(), block_table.stride(0), kv_lens.data_ptr(),
             B, Hq, Hkv, T, int(max_kv_len), d, block_size, k_pool.shape[0] // block_size,
             _strides(q), pool_strides, _strides(O), _strides(L), int(bool(is_causal)),
-            1.0 / math.sqrt(d), ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
-            _lib.stream_of(q)))
+            1.0 / math.sqrt(d), ws.data_ptr() if ws is not None else None,
+            ws.numel() if ws is not None else 0, stream))
     return (O, L) if return_lse else O
+
+
+_WS_BYTES = {}
+
+
+def _paged_ws_bytes(*dims):
+    n = _WS_BYTES.get(dims)
+    if n is None:
+        n = _lib.load().mi_fa2_fwd_paged_workspace_size(*dims)
+        if len(_WS_BYTES) >= _MEMO_MAX:
+            _WS_BYTES.clear()
+        _WS_BYTES[dims] = n
+    return n
 
 
 def fa2_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, is_causal=False,
@@ -257,12 +382,12 @@ def fa2_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, is_causal=Fals
     assert O.shape == q.shape and O.dtype == q.dtype and _dims_ok(O)
     L = torch.empty((Hq, total_q), device=q.device, dtype=torch.float32)
     lib = _lib.load()
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device) as stream:
         _lib.check(lib.mi_fa2_fwd_varlen(
             _lib.DTYPES[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(),
             L.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), B, Hq, Hkv,
             int(max_seqlen_q), d, _strides(q), _strides(k), _strides(v), _strides(O),
-            _strides(L), int(bool(is_causal)), 1.0 / math.sqrt(d), _lib.stream_of(q)))
+            _strides(L), int(bool(is_causal)), 1.0 / math.sqrt(d), stream))
     return (O, L) if return_lse else O
 
 
@@ -303,15 +428,15 @@ def fa2_paged_varlen(q, k_pool, v_pool, cu_seqlens_q, block_table, kv_lens, max_
     assert O.shape == q.shape and O.dtype == q.dtype and _dims_ok(O)
     L = torch.empty((Hq, total_q), device=q.device, dtype=torch.float32) if return_lse else None
     lib = _lib.load()
-    pool_strides = (_lib.ctypes.c_int64 * 2)(*k_pool.stride()[:2])
-    with torch.cuda.device(q.device):
+    pool_strides = _pool_strides(k_pool)
+    with _lib.on_device(q.device) as stream:
         _lib.check(lib.mi_fa2_fwd_paged_varlen(
             _lib.DTYPES[q.dtype], q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), O.data_ptr(),
             L.data_ptr() if L is not None else None, cu_seqlens_q.data_ptr(),
             block_table.data_ptr(), block_table.stride(0), kv_lens.data_ptr(), B, Hq, Hkv,
             int(max_seqlen_q), int(max_kv_len), d, block_size, k_pool.shape[0] // block_size,
             _strides(q), pool_strides, _strides(O), _strides(L) if L is not None else None,
-            int(bool(is_causal)), 1.0 / math.sqrt(d), _lib.stream_of(q)))
+            int(bool(is_causal)), 1.0 / math.sqrt(d), stream))
     return (O, L) if return_lse else O
 
 
@@ -338,7 +463,11 @@ def fa2_combine(part_o, part_lse, n_parts=None, out_dtype=torch.bfloat16, return
     if n_parts is not None:
         assert n_parts.dtype == torch.int32 and n_parts.shape == (R,) and n_parts.is_contiguous()
         assert n_parts.device == part_o.device
-    if any(st % 2 for st in part_o.stride()[:-1]) or part_o.data_ptr() % 8:
+    if part_o.data_ptr() % 8:
+        # a fresh allocation: .contiguous() would hand back an already-contiguous view as it is,
+        # still misaligned for the kernel's paired 8-byte loads
+        part_o = part_o.clone(memory_format=torch.contiguous_format)
+    elif any(st % 2 for st in part_o.stride()[:-1]):
         part_o = part_o.contiguous()
     O = torch.empty((R, H, d), device=part_o.device, dtype=out_dtype)
     L = torch.empty((R, H), device=part_o.device, dtype=torch.float32) if return_lse else None

@@ -22,7 +22,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     names = declared_symbols()
-    assert len(names) == 17
+    assert len(names) == 19
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_lib.SIGNATURES)
@@ -40,6 +40,34 @@ def test_version_and_clean_error_state():
     lib = _lib.load()
     assert lib.mi_fa2_version().decode().startswith("mi_fa2 ")
     assert "gfx950" in lib.mi_fa2_version().decode()
+
+
+@pytest.mark.parametrize("cus,xcds,mapped,paged,dense", [
+    (256, 8, 8, 768, 512),   # MI355X: the tuned sizes
+    (32, 1, 1, 96, 64),      # one XCD of it (a CPX partition)
+    (64, 2, 2, 192, 128),
+    (80, 3, 1, 240, 160),    # an XCD count that is not a power of two: no XCD mapping
+])
+def test_launch_plan_follows_the_device_topology(cus, xcds, mapped, paged, dense, monkeypatch):
+    # the grid sizes and the XCD mapping come from the device's CU and XCD counts, not from
+    # constants; the MI355X case keeps the sizes the kernels were tuned at
+    monkeypatch.delenv("MI_FA2_DECODE_WGS", raising=False)
+    pl = _lib.launch_plan(cus, xcds)
+    assert pl == {"num_cus": cus, "num_xcds": xcds, "xcds_mapped": mapped,
+                  "decode_work_groups_paged": paged, "decode_work_groups_dense": dense}
+
+
+def test_launch_plan_and_clock_stamp_reject_bad_arguments():
+    lib = _lib.load()
+    assert lib.mi_fa2_launch_plan(256, 8, None) == 1
+    assert "out is NULL" in lib.mi_fa2_last_error().decode()
+    assert lib.mi_fa2_clock_stamp(None, 8, 500, None) == 1
+    assert lib.mi_fa2_clock_stamp(16, 0, 500, None) == 1
+    assert "n_groups" in lib.mi_fa2_last_error().decode()
+    assert lib.mi_fa2_clock_stamp(16, 8, 0, None) == 1
+    assert "spin_ticks" in lib.mi_fa2_last_error().decode()
+    assert lib.mi_fa2_clock_stamp(12, 8, 500, None) == 1
+    assert "aligned" in lib.mi_fa2_last_error().decode()
 
 
 def test_workspace_sizes():
@@ -143,6 +171,36 @@ def test_overlapping_key_rows_are_rejected():
     rc = lib.mi_fa2_fwd_paged(0, 16, 16, 16, 16, None, 16, 8, 16, 1, 12, 2, 1, 64, 128, 16, 10,
                               st, ps, st, None, 0, 0.1, None, 0, None)
     assert rc == 1 and "below head_dim" in lib.mi_fa2_last_error().decode()
+
+
+def test_prefill_rejects_key_strides_past_its_32_bit_load_extents():
+    # the prefill kernel loads up to 64 K/V rows per buffer resource (rows x 2 bytes x stride in a
+    # 32-bit extent): token strides of 2^24 elements or more are refused in every prefill entry
+    # point, before anything touches a device
+    lib = _lib.load()
+    big = 1 << 24
+    st = (ctypes.c_int64 * 4)(8192, 1024, 128, 1)
+    kst = (ctypes.c_int64 * 4)(big * 8, big, big, 1)
+    rc = lib.mi_fa2_fwd(0, 16, 16, 16, 16, None, None, 1, 12, 2, 8, 8, 128, st, kst, kst, st, None,
+                        1, 0.1, None, 0, None)
+    assert rc == 2 and "2^24" in lib.mi_fa2_last_error().decode()
+    s2 = (ctypes.c_int64 * 2)(1536, 128)
+    k2 = (ctypes.c_int64 * 2)(big, 128)
+    cu = 16
+    rc = lib.mi_fa2_fwd_varlen(0, 16, 16, 16, 16, None, cu, cu, 1, 12, 2, 8, 128, s2, k2, k2, s2,
+                               None, 1, 0.1, None)
+    assert rc == 2 and "2^24" in lib.mi_fa2_last_error().decode()
+    rc = lib.mi_fa2_fwd_paged(0, 16, 16, 16, 16, None, 16, 8, 16, 1, 12, 2, 8, 64, 128, 16, 10,
+                              st, k2, st, None, 1, 0.1, None, 0, None)
+    assert rc == 2 and "2^24" in lib.mi_fa2_last_error().decode()
+    rc = lib.mi_fa2_fwd_paged_varlen(0, 16, 16, 16, 16, None, cu, 16, 8, 16, 1, 12, 2, 8, 64, 128,
+                                     16, 10, s2, k2, s2, None, 1, 0.1, None)
+    assert rc == 2 and "2^24" in lib.mi_fa2_last_error().decode()
+    # a decode (one query) keeps its own, looser bound (16-token runs: 2^26)
+    rc = lib.mi_fa2_fwd_paged(0, 16, 16, 16, 16, None, 16, 8, 16, 1, 12, 2, 1, 64, 128, 16, 10,
+                              st, (ctypes.c_int64 * 2)(1 << 26, 128), st, None, 0, 0.1, None, 0,
+                              None)
+    assert rc == 2 and "2^26" in lib.mi_fa2_last_error().decode()
 
 
 def test_paged_rejects_bad_block_size():

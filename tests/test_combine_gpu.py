@@ -99,3 +99,18 @@ def test_merge_without_counts_uses_every_partial_and_strided_outputs():
             None, None, _lib.stream_of(view)))
     torch.cuda.synchronize()
     assert (view == 0).all() and (big[:, 0::2] == 7.0).all()
+
+
+def test_misaligned_contiguous_partials_are_copied_not_refused():
+    # a contiguous view that starts 4 bytes into its buffer: the wrapper copies it to an aligned
+    # allocation for the kernel's 8-byte loads instead of passing it on (and being refused)
+    from kernels.fa2 import fa2_combine
+    po, pl, n_parts, want, want_l = build(4, max_parts=2)
+    flat = torch.empty(po.numel() + 1, dtype=torch.float32, device="cuda")
+    view = flat[1:].view(po.shape)
+    view.copy_(po.cuda())
+    assert view.is_contiguous() and view.data_ptr() % 8 == 4
+    announce("[gpu] combine: contiguous partials at a 4-byte offset")
+    o = fa2_combine(view, pl.cuda(), n_parts.cuda(), torch.float32)
+    torch.cuda.synchronize()
+    assert (o.cpu() - want).abs().max().item() < 1e-5

@@ -308,3 +308,21 @@ def test_long_sequence_on_a_large_host_table_pool_is_accepted():
     assert len(c._block_tables[s]) == 2500 and c.free_block_count() == 500
     with pytest.raises(RuntimeError, match="exhausted"):
         c.ensure_capacity(s, 3001 * 16)
+
+
+def test_concurrency_summary_reports_peak_active_and_kv_utilisation():
+    # metrics/benchmark_concurrency.py:57-76,151-159,176: the peak number of active chats and the
+    # peak tokens held by the chats' conversations as a share of the cache's capacity
+    eng = _mixed_engine(64)
+    g = torch.Generator().manual_seed(3)
+    lens = (7, 40, 3, 21)
+    prompts = [torch.randint(0, TINY.vocab_size, (n,), generator=g).tolist() for n in lens]
+    summary = run_concurrent_chats(eng, prompts, reply_tokens=4)
+    assert summary["peak_active"] == 4  # every prompt joins the first mixed step
+    held = sum(lens) + len(lens) * (4 + 1)  # prompts, 4-token replies and the separator
+    assert summary["kv_util"] == pytest.approx(100.0 * held / (64 * 16))
+    # one prompt per tick (the reference's schedule) keeps fewer chats active at once
+    eng = _engine(64)
+    summary = run_concurrent_chats(eng, prompts, reply_tokens=4)
+    assert 1 <= summary["peak_active"] <= 4
+    assert summary["kv_util"] == pytest.approx(100.0 * held / (64 * 16))

@@ -218,3 +218,43 @@ def test_general_kernel_is_deterministic():
     b = FlashAttention2Function.apply(q, k, v, True, None)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+ALL_DIMS = (16, 32, 64, 128, 256)
+
+
+@pytest.mark.parametrize("d", ALL_DIMS, ids=[f"d{x}" for x in ALL_DIMS])
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+def test_staged_kernel_every_head_dim_pair(dtype, d):
+    """Every (d, d_v) pair on the LDS-staged general kernel (64 query rows per work-group, K/V
+    staged in LDS): B=4, Hq=16, T=256 is 256 such work-groups, which reaches it on MI355X's 256
+    CUs.  Covers its 16-bit d=16 path (16x16x16 scores), the 16-bit and fp32 instantiations
+    without the register prefetch ((d + d_v) x element size > 512 bytes, e.g. bf16 256/256 and
+    fp32 256/256 with about 130 KB of LDS), and d_v = 256; causal and not, ragged rows."""
+    from kernels import _lib
+    assert 4 * 16 * 4 >= _lib.launch_plan()["num_cus"], "shape must reach the staged kernel"
+    B, Hq, Hkv, T, S = 4, 16, 4, 256, 300
+    lens = [300, 263, 256, 200]
+    for d_v in ALL_DIMS:
+        if dtype != torch.float32 and d == d_v == 128:
+            continue  # the MFMA prefill kernel's shape, covered by tests/test_fa2_gpu.py
+        g = torch.Generator().manual_seed(d * 1000 + d_v)
+        q = rand((B, Hq, T, d), g, dtype)
+        k = rand((B, Hkv, S, d), g, dtype)
+        v = rand((B, Hkv, S, d_v), g, dtype)
+        for b, n in enumerate(lens):
+            k[b, :, n:] = PAD_VALUE
+            v[b, :, n:] = PAD_VALUE
+        for causal in (True, False):
+            announce(f"[gpu] general staged: d={d} d_v={d_v} {dtype} causal={causal}")
+            out, lse = fa2_forward(q.to(DEV), k.to(DEV), v.to(DEV), causal,
+                                   torch.tensor(lens, dtype=torch.int32, device=DEV),
+                                   return_lse=True)
+            torch.cuda.synchronize()
+            check_close(out, sdpa.attention_ref(q, k, v, causal, lens), dtype,
+                        f"staged d={d} d_v={d_v} causal={causal}")
+            want = sdpa.lse_ref(q, k, causal, lens)
+            fin = torch.isfinite(want)
+            assert torch.equal(fin, torch.isfinite(lse.cpu()))
+            bar = 1e-4 if dtype == torch.float32 else math.log1p(2.0 ** -8) + 1e-3
+            assert (lse.cpu()[fin] - want[fin]).abs().max().item() < bar

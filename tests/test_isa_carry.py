@@ -77,9 +77,18 @@ def _reads_m0(line):
     return any(re.search(r"\bm0\b", o) for o in ops[1:])
 
 
+_LABEL = re.compile(r"^([.\w$]+):")
+_BRANCH = re.compile(r"\s+(s_branch|s_cbranch_\w+)\s+([.\w$]+)")
+_END_OF_FLOW = re.compile(r"\s+(s_branch|s_endpgm|s_setpc_b64)\b")
+
+
 def m0_hazards(asm):
-    """(line, reader, writer) for every m0 read outside the inline assembly whose last m0 write
-    (scanning back through the code) is inside an inline-assembly statement."""
+    """(line, reader, writer) for every m0 read outside the inline assembly that some control-flow
+    path reaches with its last m0 write inside an inline-assembly statement.  From each read the
+    code is scanned backwards; at a basic-block label the scan follows every predecessor: the
+    fall-through from the line above (unless that ends the flow: s_branch, s_endpgm, s_setpc) and
+    every branch that targets the label (loop back edges included).  A function's own entry label
+    (not a local .L label) ends a path with no write."""
     lines = asm.split("\n")
     in_asm = [False] * len(lines)
     state = False
@@ -89,14 +98,46 @@ def m0_hazards(asm):
         elif ";;#ASMEND" in t:
             state = False
         in_asm[i] = state
+    branches_to = {}
+    for i, t in enumerate(lines):
+        m = _BRANCH.match(t)
+        if m:
+            branches_to.setdefault(m.group(2), []).append(i)
+
+    def last_writes(start):
+        """Indices of the last m0 write on every path ending just above line `start`."""
+        found, seen, todo = set(), set(), [start]
+        while todo:
+            j = todo.pop() - 1
+            while j >= 0:
+                t = lines[j]
+                if _M0_WRITE.match(t):
+                    found.add(j)
+                    break
+                lm = _LABEL.match(t)
+                if lm:
+                    label = lm.group(1)
+                    if not label.startswith(".L"):
+                        break  # a function's entry: no write on this path
+                    if label in seen:
+                        break
+                    seen.add(label)
+                    todo.extend(b for b in branches_to.get(label, []))
+                    k = j - 1
+                    while k >= 0 and (not lines[k].strip() or lines[k].lstrip().startswith(";")):
+                        k -= 1
+                    if k >= 0 and _END_OF_FLOW.match(lines[k]):
+                        break  # no fall-through into this label
+                j -= 1
+        return found
+
     bad = []
     for i, line in enumerate(lines):
         if in_asm[i] or not _reads_m0(line):
             continue
-        for j in range(i - 1, -1, -1):
-            if _M0_WRITE.match(lines[j]):
-                if in_asm[j]:
-                    bad.append((i, line.strip(), lines[j].strip()))
+        for j in sorted(last_writes(i)):
+            if in_asm[j]:
+                bad.append((i, line.strip(), lines[j].strip()))
                 break
     return bad
 
@@ -128,6 +169,23 @@ def test_checker_flags_m0_set_by_inline_assembly():
     # the compiler resets m0 before its own use: fine; m0 as a destination is not a read
     assert m0_hazards("\t;;#ASMSTART\n\ts_mov_b32 m0, s9\n\t;;#ASMEND\n\ts_mov_b32 m0, s2\n"
                       "\tbuffer_load_dword v1, v2, s[4:7], 0 offen lds\n") == []
+    # a loop: the read at the loop head is preceded in text by the compiler's own write, but the
+    # back edge brings it the value the inline assembly at the loop's end wrote
+    loop = ("kern:\n\ts_mov_b32 m0, s2\n.LBB0_1:\n"
+            "\tbuffer_load_dword v1, v2, s[4:7], 0 offen lds\n"
+            "\t;;#ASMSTART\n\ts_mov_b32 m0, s9\n\t;;#ASMEND\n"
+            "\ts_cbranch_scc1 .LBB0_1\n\ts_endpgm\n")
+    assert [b[0] for b in m0_hazards(loop)] == [3]
+    # the same loop with the compiler's write inside it, ahead of the read: fine
+    assert m0_hazards(loop.replace(".LBB0_1:\n", ".LBB0_1:\n\ts_mov_b32 m0, s2\n")) == []
+    # a branch target reached only by a jump from code whose last write is the compiler's: fine,
+    # even though the text right above the label ends with an assembly write and an s_branch
+    jump = ("kern:\n\ts_mov_b32 m0, s2\n\ts_cbranch_scc0 .LBB0_2\n"
+            "\t;;#ASMSTART\n\ts_mov_b32 m0, s9\n\t;;#ASMEND\n\ts_branch .LBB0_3\n"
+            ".LBB0_2:\n\tbuffer_load_dword v1, v2, s[4:7], 0 offen lds\n"
+            ".LBB0_3:\n\ts_endpgm\n")
+    assert m0_hazards(jump) == []
+    assert [b[0] for b in m0_hazards(jump.replace("s_branch .LBB0_3", "s_nop 0"))] == [8]
 
 
 @pytest.mark.skipif(not Path(HIPCC).exists(), reason="hipcc not available")

@@ -71,3 +71,39 @@ def test_noalloc_prefill_equals_the_workspace_entry_point():
     want, want_l = _call(False, q.cuda(), kp.cuda(), vp.cuda(), bt, lens, 700, True)
     torch.cuda.synchronize()
     assert torch.equal(got, want) and torch.equal(got_l, want_l)
+
+
+def test_noalloc_decode_allocates_no_device_memory():
+    # what the entry point is for: after a first call (which looks up the scratch's address once),
+    # calls leave the device's free memory and torch's allocations unchanged
+    q, kp, vp, tables, lens = wl.decode_paged(n_rows=16, lo=128, hi=4000, seed=3)
+    bt = wl.table_tensor(tables).cuda()
+    lens_t = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    qd, kd, vd = q.cuda(), kp.cuda(), vp.cuda()
+    B, Hq, T, d = qd.shape
+    O = torch.empty_like(qd)
+    L = torch.empty((B, Hq, T), device="cuda")
+    max_kv = bt.shape[1] * 16
+    assert _lib.load().mi_fa2_fwd_paged_workspace_size(B, Hq, kd.shape[1], T, max_kv, d) > 0
+    pool = (ctypes.c_int64 * 2)(*kd.stride()[:2])
+    qs, os_, ls = _lib.strides(qd), _lib.strides(O), _lib.strides(L)
+    stream = _lib.stream_of(qd)
+    lib = _lib.load()
+
+    def call():
+        _lib.check(lib.mi_fa2_fwd_paged_noalloc(
+            0, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), O.data_ptr(), L.data_ptr(),
+            bt.data_ptr(), bt.stride(0), lens_t.data_ptr(), B, Hq, kd.shape[1], T, max_kv, d, 16,
+            kd.shape[0] // 16, qs, pool, os_, ls, 0, 1.0 / math.sqrt(d), stream))
+
+    announce("[gpu] no-alloc paged decode: device memory before and after")
+    call()
+    torch.cuda.synchronize()
+    free0, alloc0 = torch.cuda.mem_get_info()[0], torch.cuda.memory_allocated()
+    for _ in range(3):
+        call()
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated() == alloc0
+    assert torch.cuda.mem_get_info()[0] >= free0
+    want, _ = _call(False, qd, kd, vd, bt, lens_t, max_kv, False)
+    assert torch.equal(O, want)
