@@ -78,8 +78,10 @@ def _ramp(fn, ms):
 def _time_gpu(fn, steps, warmup, ramp_ms=None):
     """(average ms per call of fn() over exactly `steps` calls, the shader clock they ran at):
     HIP events on the current stream, after the sustained-clock ramp (`_ramp`) and `warmup`
-    untimed calls.  Clock stamps (kernels.clock.ClockStamp) on the same stream right before the
-    start event and right after the end event give the clock of the timed calls, per XCD.
+    untimed calls.  The timed calls run with the kernels' clock probe on (kernels.clock): the
+    first work-group on each XCD of every attention launch counts its own shader cycles and
+    real-time ticks, which give the clock the timed kernels ran at (None if no attention kernel
+    ran).
 
     Python's garbage collector is run first and disabled from the ramp to the end of the timed
     calls (as timeit does): the host enqueues a call in 35-50 us against a 50-70 us kernel, so a
@@ -87,8 +89,8 @@ def _time_gpu(fn, steps, warmup, ramp_ms=None):
     make one likely -- would leave the GPU idle inside it (seen: 0.7-1.05 ms per call instead of
     0.061), and one between the ramp and the timed calls would let the clock fall back."""
     import torch
-    from kernels.clock import ClockStamp
-    stamp = ClockStamp()
+    from kernels.clock import ClockProbe
+    probe = ClockProbe()
     gc.collect()
     enabled = gc.isenabled()
     gc.disable()
@@ -99,17 +101,16 @@ def _time_gpu(fn, steps, warmup, ramp_ms=None):
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
-        stamp.before()
-        start.record()
-        for i in range(steps):
-            fn(i)
-        end.record()
-        stamp.after()
+        with probe:
+            start.record()
+            for i in range(steps):
+                fn(i)
+            end.record()
         torch.cuda.synchronize()
     finally:
         if enabled:
             gc.enable()
-    return start.elapsed_time(end) / steps, stamp.result()
+    return start.elapsed_time(end) / steps, probe.result()
 
 
 def bench_prefill(steps, warmup, seq_len=4096, cold=False):

@@ -85,20 +85,19 @@ typedef struct mi_fa2_plan {
 MI_FA2_API int mi_fa2_launch_plan(int32_t num_cus, int32_t num_xcds, mi_fa2_plan* out);
 
 /*
- * Measurement support, no counterpart in the reference (which publishes no kernel timings): reads
- * the shader clock on `stream`.  Launches n_groups single-wave work-groups; work-group w reads its
- * CU's shader-cycle counter (s_memtime) and the 100 MHz real-time counter (s_memrealtime), spins
- * until the latter has advanced by spin_ticks (10 ns each), reads both again and writes
- *   out[5w] = cycles0, out[5w+1] = ticks0, out[5w+2] = cycles1, out[5w+3] = ticks1,
- *   out[5w+4] = its XCD id;
- * its CU's clock is (cycles1 - cycles0) / (ticks1 - ticks0) x 100 MHz.  The shader-cycle count is
- * per CU and stops while the CU is clock-gated, so readings of different work-groups are never
- * differenced.  A reading right before and one right after a timed region on the same stream
- * bracket the clock that region ran at.  out: device memory, 8-byte aligned, 5 x n_groups
- * uint64 (n_groups 1..1024, spin_ticks 1..100000).
+ * Measurement support, no counterpart in the reference (which publishes no kernel timings): the
+ * shader clock the attention kernels actually run at.  With probe set (device memory, 16 uint64,
+ * zeroed by the caller), every later prefill, decode and general-kernel launch adds, for thread 0
+ * of each of its first 8 work-groups, the shader cycles its CU counted (s_memtime) and the
+ * 100 MHz real-time ticks (s_memrealtime) between that work-group's start and end to
+ * probe[2 x] and probe[2 x + 1], x = the work-group's XCD (0-7; the first 8 work-groups of a
+ * launch run one per XCD on MI355X).  The clock XCD x ran those kernels at is
+ * probe[2 x] / probe[2 x + 1] x 100 MHz.  The counts of different CUs are never compared (each
+ * CU counts its own clocks and stops while clock-gated).  probe NULL turns it off (the default);
+ * the setting is process-wide and applies to launches made after the call.  Measurement only:
+ * calls that overlap in time accumulate into the same sums.
  */
-MI_FA2_API int mi_fa2_clock_stamp(uint64_t* out, int32_t n_groups, int32_t spin_ticks,
-                                  mi_fa2_stream_t stream);
+MI_FA2_API int mi_fa2_set_clock_probe(uint64_t* probe);
 
 /*
  * Padded forward.  Replaces FlashAttention2Function.forward (kernels/fa2.py:164-214) and the Triton

@@ -16,7 +16,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 OUT = PKG / "kernels" / "libmi_fa2.so"
-SOURCES = ["fa2_prefill.hip", "fa2_decode.hip", "fa2_general.hip", "fa2_merge.hip", "rope_kv.hip", "sample.hip", "step_meta.hip", "model_ops.hip", "device_info.hip", "fa2_capi.cpp"]
+SOURCES = ["fa2_prefill.hip", "fa2_decode.hip", "fa2_general.hip", "fa2_merge.hip", "rope_kv.hip", "sample.hip", "step_meta.hip", "model_ops.hip", "fa2_capi.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -24,7 +25,6 @@ int sample_chunks(int vocab);
 hipError_t launch_step_meta(const StepMetaParams& p, hipStream_t stream);
 hipError_t launch_add_rmsnorm(const ModelOpParams& p, int dtype, hipStream_t stream);
 hipError_t launch_silu_mul(const ModelOpParams& p, int dtype, hipStream_t stream);
-hipError_t launch_clock_stamp(uint64_t* out, int n_groups, int spin_ticks, hipStream_t stream);
 }  // namespace mi_fa2
 
 using mi_fa2::FwdParams;
@@ -114,12 +114,16 @@ int plan_of_current_device(Plan* out) {
   return MI_FA2_OK;
 }
 
-// Fills the launch's device fields (CU count, XCD mapping) from the current device.
+// The clock probe set by mi_fa2_set_clock_probe (measurement only; null: off).
+std::atomic<uint64_t*> g_clock_probe{nullptr};
+
+// Fills the launch's device fields (CU count, XCD mapping, clock probe) from the current device.
 int set_device(FwdParams& p, Plan* plan = nullptr) {
   Plan pl;
   if (int rc = plan_of_current_device(&pl)) return rc;
   p.n_cus = pl.cus;
   p.xcd_log2 = pl.xcd_log2;
+  p.clock_probe = g_clock_probe.load(std::memory_order_relaxed);
   if (plan) *plan = pl;
   return MI_FA2_OK;
 }
@@ -373,17 +377,11 @@ int mi_fa2_launch_plan(int32_t num_cus, int32_t num_xcds, mi_fa2_plan* out) {
   return ok();
 }
 
-int mi_fa2_clock_stamp(uint64_t* out, int32_t n_groups, int32_t spin_ticks,
-                       mi_fa2_stream_t stream) {
-  if (!out) return fail(MI_FA2_ERR_INVALID, "out is NULL");
-  if (n_groups <= 0 || n_groups > 1024)
-    return fail(MI_FA2_ERR_INVALID, "n_groups %d: 1 to 1024 work-groups", n_groups);
-  if (spin_ticks < 1 || spin_ticks > 100000)
-    return fail(MI_FA2_ERR_INVALID, "spin_ticks %d: 1 to 100000 (10 ns each)", spin_ticks);
-  if (reinterpret_cast<uintptr_t>(out) % 8)
-    return fail(MI_FA2_ERR_INVALID, "out is not 8-byte aligned");
-  return launched(mi_fa2::launch_clock_stamp(out, n_groups, spin_ticks,
-                                             reinterpret_cast<hipStream_t>(stream)));
+int mi_fa2_set_clock_probe(uint64_t* probe) {
+  if (reinterpret_cast<uintptr_t>(probe) % 8)
+    return fail(MI_FA2_ERR_INVALID, "probe is not 8-byte aligned");
+  g_clock_probe.store(probe, std::memory_order_relaxed);
+  return ok();
 }
 
 size_t mi_fa2_fwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv,

@@ -126,6 +126,9 @@ struct FwdParams {
   // device by the C ABI: they size grids and map work-groups to XCDs
   int32_t n_cus;
   int32_t xcd_log2;
+  // measurement only (mi_fa2_set_clock_probe), usually null: [16] uint64, the shader cycles and
+  // 100 MHz ticks spent by the first work-groups of each launch, summed per XCD
+  uint64_t* clock_probe;
 };
 
 // Everything the fused RoPE + KV-write launch needs (rope_kv.hip).
@@ -298,6 +301,28 @@ __device__ __forceinline__ int opaque(int x) {
 __device__ __forceinline__ float fmax3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Clock probe (measurement only): with p.clock_probe set, thread 0 of each of a launch's first 8
+// work-groups (one per XCD on MI355X) reads its CU's shader-cycle counter (s_memtime: the CU's own
+// clocks) and the 100 MHz real-time counter (s_memrealtime) when it starts and when it is done,
+// and its XCD's pair of sums, probe[2 * xcd] and probe[2 * xcd + 1], takes the differences (the
+// start readings are subtracted at the start and the end readings added at the end, modulo 2^64,
+// so that nothing is held in registers in between): their ratio is the clock that XCD ran the
+// kernel at.  The counts of different CUs are never compared.  Off (a null pointer), it costs a
+// uniform branch at the start and at the end.
+__device__ __forceinline__ void probe_mark(uint64_t* probe, uint32_t wg_linear, bool end) {
+  if (probe != nullptr && wg_linear < 8 && threadIdx.x == 0) {
+    const uint64_t c = __builtin_amdgcn_s_memtime();
+    const uint64_t t = __builtin_amdgcn_s_memrealtime();
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= 7u;
+    atomicAdd(reinterpret_cast<unsigned long long*>(probe + 2 * xcc),
+              (unsigned long long)(end ? c : 0 - c));
+    atomicAdd(reinterpret_cast<unsigned long long*>(probe + 2 * xcc + 1),
+              (unsigned long long)(end ? t : 0 - t));
+  }
+}
 
 // Keys held by row b, clamped to [0, cap].
 __device__ __forceinline__ int clamp_len(int n, int cap) { return n < 0 ? 0 : (n > cap ? cap : n); }

@@ -300,6 +300,7 @@ __global__ __launch_bounds__(256, DcShape<MODE>::kOcc) void fa2_decode_kernel(co
   float* red_m = red + kDcWaves * p.group * kRedPitch;
   float* red_l = red_m + kDcWaves * p.group;
   int* R = reinterpret_cast<int*>(red_l + kDcWaves * p.group);
+  probe_mark(p.clock_probe, blockIdx.x, false);
 
   dc_row_prefix(p, R);
   const int64_t N = (int64_t)R[p.B] * p.Hkv;
@@ -474,6 +475,7 @@ __global__ __launch_bounds__(256, DcShape<MODE>::kOcc) void fa2_decode_kernel(co
       kb = kb2;
     }
   }
+  probe_mark(p.clock_probe, blockIdx.x, true);
 }
 
 // Merges the partials of items that were cut by work-group boundaries (their count is recorded by

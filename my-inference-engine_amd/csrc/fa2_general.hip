@@ -154,6 +154,8 @@ __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_kernel(FwdParams p
   constexpr int KP = D + kEl16, VP = DV + kEl16;
   __shared__ __attribute__((aligned(16))) T kl[kGenKeys * KP];
   __shared__ __attribute__((aligned(16))) T vl[kGenKeys * VP];
+  const uint32_t wg_linear = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  probe_mark(p.clock_probe, wg_linear, false);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
@@ -357,6 +359,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_kernel(FwdParams p
   if (p.lse && g == 0)
     p.lse[b * p.l_sb + h * p.l_sh + (int64_t)q * p.l_st] =
         l_tot > 0.f ? (m_run + __builtin_log2f(l_tot)) * kLn2 : -INFINITY;
+  probe_mark(p.clock_probe, wg_linear, true);  // thread 0's query row always exists
 }
 
 // Key-split variant for launches that would leave the chip idle: fewer query rows than a
@@ -376,6 +379,8 @@ __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_split_kernel(FwdPa
   __shared__ float sm_m[kGenWaves][kGenRows];
   __shared__ float sm_l[kGenWaves][kGenRows];
   __shared__ f32x4 sm_o[kGenWaves][kVB][64];
+  const uint32_t wg_linear = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  probe_mark(p.clock_probe, wg_linear, false);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
@@ -521,6 +526,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_split_kernel(FwdPa
   if (p.lse && wave == 0 && g == 0)
     p.lse[b * p.l_sb + h * p.l_sh + (int64_t)q * p.l_st] =
         L > 0.f ? (M + __builtin_log2f(L)) * kLn2 : -INFINITY;
+  probe_mark(p.clock_probe, wg_linear, true);  // thread 0's query row always exists
 }
 
 }  // namespace mi_fa2

@@ -195,6 +195,7 @@ template <typename E, int MODE>
 __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdParams p, int n_qt_max,
                                                                     const ItemMap map) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
+  probe_mark(p.clock_probe, blockIdx.x, false);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -787,6 +788,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   if (ks == 0 && p.lse && g == 0 && qrow < T_b)
     p.lse[l_off + (int64_t)qrow * p.l_st] =
         l_tot > 0.f ? (m_run + __builtin_log2f(l_tot)) * kLn2 : -INFINITY;
+  probe_mark(p.clock_probe, blockIdx.x, true);
 }
 
 template <typename E, int MODE>

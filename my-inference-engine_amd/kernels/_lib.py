@@ -37,7 +37,7 @@ SIGNATURES = {
     "mi_fa2_version": (ctypes.c_char_p, []),
     "mi_fa2_last_error": (ctypes.c_char_p, []),
     "mi_fa2_launch_plan": (_i32, [_i32, _i32, ctypes.POINTER(Plan)]),
-    "mi_fa2_clock_stamp": (_i32, [_p, _i32, _i32, _p]),
+    "mi_fa2_set_clock_probe": (_i32, [_p]),
     "mi_fa2_fwd_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "mi_fa2_fwd": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
                           _p, _p, _p, _p, _p, _i32, _f32, _p, _sz, _p]),

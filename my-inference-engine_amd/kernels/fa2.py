@@ -213,8 +213,9 @@ def _plan_padded(Q, K, V, is_causal):
     return pl
 
 
-def _run_padded(Q, K, V, is_causal, kv_lens):
-    """The padded forward: (O, L), launched on the current stream of Q's device."""
+def _run_padded(Q, K, V, is_causal, kv_lens, want_lse=True):
+    """The padded forward: (O, L), launched on the current stream of Q's device.  want_lse=False
+    skips L (None is returned in its place): the kernels then store no LSE."""
     key = (Q.shape, Q.stride(), K.shape, K.stride(), V.shape, V.stride(), Q.dtype, K.dtype,
            V.dtype, Q.device, K.device, V.device, bool(is_causal))
     pl = _PADDED.get(key)
@@ -239,7 +240,8 @@ def _run_padded(Q, K, V, is_causal, kv_lens):
         tail = (_strides(q), _strides(k), _strides(v)) + tail[3:]
     dev = pl.dev
     O = torch.empty(pl.o_shape, device=dev, dtype=Q.dtype)
-    L = torch.empty(pl.l_shape, device=dev, dtype=torch.float32)
+    L = torch.empty(pl.l_shape, device=dev, dtype=torch.float32) if want_lse else None
+    lp = L.data_ptr() if want_lse else None
     lib = _lib.load()
     lens = kv_lens.data_ptr() if kv_lens is not None else None
     with _lib.on_device(dev) as stream:
@@ -247,13 +249,13 @@ def _run_padded(Q, K, V, is_causal, kv_lens):
             ws = _workspace(pl.ws_bytes, dev)
             _lib.check(lib.mi_fa2_fwd(
                 pl.dtype_code, q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(),
-                L.data_ptr(), lens, *pl.head, *tail,
+                lp, lens, *pl.head, *tail,
                 ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
                 stream))
         else:
             _lib.check(lib.mi_fa2_fwd_general(
                 pl.dtype_code, q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(),
-                L.data_ptr(), lens, *pl.head, *tail, stream))
+                lp, lens, *pl.head, *tail, stream))
     return O, L
 
 
@@ -272,11 +274,12 @@ class FlashAttention2Function(torch.autograd.Function):
     def apply(cls, Q, K, V, is_causal=False, kv_lens=None):
         """Same call and result as torch.autograd.Function.apply.  The reference's Function has a
         forward only (kernels/fa2.py:164-214): an autograd node is recorded when an input
-        requires grad, as before; otherwise (inference, every call of the engine) the forward runs
-        directly, without the node machinery's host cost (several microseconds per call)."""
+        requires grad, as before, and L is saved on it; otherwise (inference, every call of the
+        engine) no node exists to save L on, so the forward runs directly and computes O alone,
+        without the node machinery's host cost (several microseconds per call)."""
         if torch.is_grad_enabled() and (Q.requires_grad or K.requires_grad or V.requires_grad):
             return super().apply(Q, K, V, is_causal, kv_lens)
-        return _run_padded(Q, K, V, is_causal, kv_lens)[0]
+        return _run_padded(Q, K, V, is_causal, kv_lens, want_lse=False)[0]
 
 
 def fa2_forward(Q, K, V, is_causal=False, kv_lens=None, return_lse=False):
@@ -331,16 +334,17 @@ def fa2_paged(q, k_pool, v_pool, block_table, kv_lens, *, block_size=16, max_kv_
     assert _dims_ok(k_pool) and _dims_ok(v_pool), "pools need 16-byte aligned token rows"
     O = out if out is not None else torch.empty((B, Hq, T, d), device=q.device, dtype=q.dtype)
     assert O.shape == q.shape and O.dtype == q.dtype and _dims_ok(O)
-    L = torch.empty((B, Hq, T), device=q.device, dtype=torch.float32)
+    L = torch.empty((B, Hq, T), device=q.device, dtype=torch.float32) if return_lse else None
     lib = _lib.load()
     ws = _workspace(_paged_ws_bytes(B, Hq, Hkv, T, int(max_kv_len), d), q.device)
     pool_strides = _pool_strides(k_pool)
     with _lib.on_device(q.device) as stream:
         _lib.check(lib.mi_fa2_fwd_paged(
             _lib.DTYPES[q.dtype], q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), O.data_ptr(),
-            L.data_ptr(), block_table.data_ptr(), block_table.stride(0), kv_lens.data_ptr(),
-            B, Hq, Hkv, T, int(max_kv_len), d, block_size, k_pool.shape[0] // block_size,
-            _strides(q), pool_strides, _strides(O), _strides(L), int(bool(is_causal)),
+            L.data_ptr() if L is not None else None, block_table.data_ptr(), block_table.stride(0),
+            kv_lens.data_ptr(), B, Hq, Hkv, T, int(max_kv_len), d, block_size,
+            k_pool.shape[0] // block_size, _strides(q), pool_strides, _strides(O),
+            _strides(L) if L is not None else None, int(bool(is_causal)),
             1.0 / math.sqrt(d), ws.data_ptr() if ws is not None else None,
             ws.numel() if ws is not None else 0, stream))
     return (O, L) if return_lse else O
@@ -380,14 +384,15 @@ def fa2_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, is_causal=Fals
     q, k, v = _vec(q), _vec(k), _vec(v)
     O = out if out is not None else torch.empty((total_q, Hq, d), device=q.device, dtype=q.dtype)
     assert O.shape == q.shape and O.dtype == q.dtype and _dims_ok(O)
-    L = torch.empty((Hq, total_q), device=q.device, dtype=torch.float32)
+    L = torch.empty((Hq, total_q), device=q.device, dtype=torch.float32) if return_lse else None
     lib = _lib.load()
     with _lib.on_device(q.device) as stream:
         _lib.check(lib.mi_fa2_fwd_varlen(
             _lib.DTYPES[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(),
-            L.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), B, Hq, Hkv,
-            int(max_seqlen_q), d, _strides(q), _strides(k), _strides(v), _strides(O),
-            _strides(L), int(bool(is_causal)), 1.0 / math.sqrt(d), stream))
+            L.data_ptr() if L is not None else None, cu_seqlens_q.data_ptr(),
+            cu_seqlens_k.data_ptr(), B, Hq, Hkv, int(max_seqlen_q), d, _strides(q), _strides(k),
+            _strides(v), _strides(O), _strides(L) if L is not None else None,
+            int(bool(is_causal)), 1.0 / math.sqrt(d), stream))
     return (O, L) if return_lse else O
 
 

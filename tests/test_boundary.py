@@ -57,17 +57,13 @@ def test_launch_plan_follows_the_device_topology(cus, xcds, mapped, paged, dense
                   "decode_work_groups_paged": paged, "decode_work_groups_dense": dense}
 
 
-def test_launch_plan_and_clock_stamp_reject_bad_arguments():
+def test_launch_plan_and_clock_probe_reject_bad_arguments():
     lib = _lib.load()
     assert lib.mi_fa2_launch_plan(256, 8, None) == 1
     assert "out is NULL" in lib.mi_fa2_last_error().decode()
-    assert lib.mi_fa2_clock_stamp(None, 8, 500, None) == 1
-    assert lib.mi_fa2_clock_stamp(16, 0, 500, None) == 1
-    assert "n_groups" in lib.mi_fa2_last_error().decode()
-    assert lib.mi_fa2_clock_stamp(16, 8, 0, None) == 1
-    assert "spin_ticks" in lib.mi_fa2_last_error().decode()
-    assert lib.mi_fa2_clock_stamp(12, 8, 500, None) == 1
+    assert lib.mi_fa2_set_clock_probe(12) == 1
     assert "aligned" in lib.mi_fa2_last_error().decode()
+    assert lib.mi_fa2_set_clock_probe(None) == 0
 
 
 def test_workspace_sizes():
