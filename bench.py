@@ -222,6 +222,14 @@ def bench_e2e(n_chats=16, reply_tokens=64, lo=32, hi=1000, seed=0, decode_graphs
         run_concurrent_chats(eng, prompts[:2], reply_tokens=2)   # warm-up (two chats, two tokens)
         res[name] = run_concurrent_chats(eng, prompts, reply_tokens)
         assert cache.free_block_count() == cache.num_blocks
+    # The reference's concurrency curve (metrics/benchmark_concurrency.py:17,204): the first n of
+    # the same chats, mixed schedule, n = 1, 2, 4, 8 (n_chats is the run above).
+    eng = Engine(model, cache, max_reply_tokens=reply_tokens, temperature=1.0, seed=seed,
+                 decode_graphs=graphs, mixed_prefill=True)
+    res["sweep"] = {n: run_concurrent_chats(eng, prompts[:n], reply_tokens)
+                    for n in (1, 2, 4, 8) if n < n_chats}
+    res["sweep"][n_chats] = res["mixed"]
+    assert cache.free_block_count() == cache.num_blocks
     return res
 
 
@@ -240,6 +248,7 @@ def e2e_line(e2e):
            "replayed as HIP graphs, tokens drawn by the fused HIP sampler"}
     rec.update(figs(m))
     rec["separate_prefill"] = figs(s)
+    rec["concurrency_sweep"] = [dict(chats=n, **figs(r)) for n, r in sorted(e2e["sweep"].items())]
     rec["workload"] = (f"Qwen2.5-1.5B architecture, random N(0,0.02) bf16 weights; 16 chats, "
                        f"prompts U[32,1000] random ids (sum {e2e['prompt_lens_sum']}), 64 tokens "
                        f"each, temperature 1, paged KV 1024 x 16-token blocks "
