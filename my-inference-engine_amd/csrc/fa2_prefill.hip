@@ -9,7 +9,10 @@
 //     +31 and key stream w/4: stream 0 takes the even 64-key tiles, stream 1 the odd ones, so two
 //     waves share every SIMD (one's softmax hides behind the other's MFMAs) and the longest causal
 //     tile is walked by two waves in parallel.  The two streams' (m, l, O) are merged in LDS at the
-//     end.
+//     end.  Launches with at least two work-groups per CU use a one-stream shape instead: 4 waves
+//     on the same 128 rows walk every tile in turn with half the LDS (64 KB), so two work-groups
+//     share a CU, the SIMD's two waves come from different tiles, and one work-group's start
+//     (item, Q, first stages) and end (stores) run under the other's key loop.
 //   * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16: the accumulator holds
 //     one query per lane (lane%32) and 16 keys per lane in registers.  That is exactly the B-operand
 //     layout of O^T += V^T P^T, so P never leaves registers and the running max / sum and the O
@@ -34,27 +37,36 @@
 //     with no per-lane predicate.  In paged mode a wave's two instructions of a tile (8 rows)
 //     share one block; the block-table entries of 16 steps are fetched with one vector load and
 //     turned into load addresses in one vector pass, each instruction reading its own back.
-//   * LDS holds two stages of (K, V) for both streams; the next 128 keys are loaded while the
-//     current ones are computed, one barrier per 128 keys.
+//   * LDS holds two stages of (K, V) for every stream; the next step's keys (128, or 64 with one
+//     stream) are loaded while the current ones are computed, one barrier per step.
 //   * Masking runs only on tiles that straddle the causal diagonal or the end of the row, and tiles
 //     past the diagonal are never loaded.  The grid is 1-D, mapped XCD-aware: query heads sharing a
 //     kv head run on the same XCDs (one L2 holds their K/V) and every XCD takes its tiles longest
 //     first, so causal work drains evenly.
 #include "fa2_common.h"
 
+#include <cstdlib>
+
 namespace mi_fa2 {
 
 constexpr int kPfRowGroups = 4;                  // 32-row query groups per work-group
-constexpr int kPfStreams = 2;                    // key streams per work-group
-constexpr int kPfWaves = kPfRowGroups * kPfStreams;
-constexpr int kPfThreads = 64 * kPfWaves;
 constexpr int kPfRows = 32 * kPfRowGroups;       // query rows per work-group
 constexpr int kPfBc = 64;                        // keys per tile (one stream's share of a step)
-constexpr int kPfStep = kPfBc * kPfStreams;      // keys per step
 constexpr int kTileBytes = kPfBc * kHeadDim * 2;       // one 64-key K or V tile in LDS (16 KB)
-constexpr int kStageBytes = kPfStreams * kTileBytes;   // K (or V) tiles of one stage
-constexpr int kVRegion = 2 * kStageBytes;              // V tiles start after both stages' K tiles
-constexpr int kLdsBytes = 2 * kVRegion;                // 128 KB
+
+// The work-group shape for NS key streams (2: the layout described above, 8 waves and 128 KB of
+// LDS, one work-group per CU; 1: 4 waves walking every tile in turn with 64 KB of LDS, so that two
+// work-groups share a CU and each one's start and end run under the other's key loop).
+template <int NS>
+struct PfShape {
+  static constexpr int kWaves = kPfRowGroups * NS;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kStep = kPfBc * NS;              // keys per step
+  static constexpr int kStage = NS * kTileBytes;        // K (or V) tiles of one stage
+  static constexpr int kVRegion = 2 * kStage;           // V tiles start after both stages' K tiles
+  static constexpr int kLds = 2 * kVRegion;             // 128 KB (NS = 2) or 64 KB (NS = 1)
+  static constexpr int kLoadsPerWave = 16 / kWaves;     // load instructions per wave and tile
+};
 constexpr float kRescaleSlack = 8.f;             // log2 units the running max may lag the true max
 constexpr float kSumLimit = 256.f;               // 2^kRescaleSlack
 
@@ -191,17 +203,21 @@ __device__ inline bool prefill_item_packed(const FwdParams& p, int w, const Item
   return r < n_qt;
 }
 
-template <typename E, int MODE>
-__global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdParams p, int n_qt_max,
-                                                                    const ItemMap map) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
+template <typename E, int MODE, int NS>
+__global__ __launch_bounds__(PfShape<NS>::kThreads, 2) void fa2_prefill_kernel(const FwdParams p,
+                                                                               int n_qt_max,
+                                                                               const ItemMap map) {
+  using Sh = PfShape<NS>;
+  constexpr int kPfStep = Sh::kStep, kStageBytes = Sh::kStage, kVRegion = Sh::kVRegion;
+  constexpr int kPfWaves = Sh::kWaves, kLpw = Sh::kLoadsPerWave;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[Sh::kLds];
   probe_mark(p.clock_probe, blockIdx.x, false);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int rg = wave % kPfRowGroups;
-  const int ks = wave / kPfRowGroups;
+  const int ks = NS == 2 ? wave / kPfRowGroups : 0;  // key stream
   int b, h, rank;
   bool real;
   if constexpr (MODE == kVarlen || MODE == kPagedVarlen)
@@ -304,21 +320,24 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   //   stream 1, step j: S(j, 1) ; PV(j-1, 1) ; softmax(j, 1)      (32 MFMAs, then VALU)
   //   (paged modes: stream 1 runs PV(j-1, 1) before S(j, 1))
   // Stage j (LDS slot j%2) therefore holds V(j,0), K(j+1,0), V(j-1,1) and K(j,1); it is loaded
-  // during step j-1, one barrier per step.
+  // during step j-1, one barrier per step.  With one stream, tile j is keys 64j .. +63, every
+  // wave runs stream 0's program and stage j holds V(j) and K(j+1).
   //
   // Staging.  Every tile is 16 load instructions of 4 rows; instruction i moves rows 4i .. 4i+3,
-  // lane l row 4i + l/16 into LDS chunk l%16, i.e. global chunk (l%16) ^ swizzle(row).
-  //   * dense and packed modes: wave w issues instructions w and w + 8 of each tile; rows 4i and
-  //     4(i+8) agree mod 16, so one offset (relative to the tile's first row, instruction h
-  //     adding 32 rows) serves both;
-  //   * paged modes: wave w issues instructions 2w and 2w + 1, rows 8w .. 8w+7 of the tile, which
-  //     lie in one block (blocks are multiples of 16 rows): one table entry and one address serve
-  //     both, and the offsets are relative to row 8w (instruction h adding 4 rows).
+  // lane l row 4i + l/16 into LDS chunk l%16, i.e. global chunk (l%16) ^ swizzle(row).  Each of
+  // the W waves (8, or 4 with one stream) issues L = 16 / W of them per tile:
+  //   * dense and packed modes: wave w issues instructions w + W*h, h < L; those rows agree
+  //     mod 16, so one offset (relative to the tile's first row, instruction h adding 4W rows)
+  //     serves all of them;
+  //   * paged modes: wave w issues instructions L*w + h, rows 4Lw .. 4Lw + 4L - 1 of the tile
+  //     (8 or 16 rows), which lie in one block (blocks are multiples of 16 rows): one table entry
+  //     and one address serve all of them, and the offsets are relative to row 4Lw (instruction h
+  //     adding 4 rows).
   const int lrow = lane >> 4;
-  int k_voff[2], v_voff[2];
+  int k_voff[kLpw], v_voff[kLpw];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int row = is_paged(MODE) ? 8 * wave + 4 * h + lrow : 4 * wave + lrow;  // swizzle row
+  for (int h = 0; h < kLpw; ++h) {
+    const int row = is_paged(MODE) ? 4 * kLpw * wave + 4 * h + lrow : 4 * wave + lrow;  // swizzle row
     const int trow = is_paged(MODE) ? 4 * h + lrow : 4 * wave + lrow;
     k_voff[h] = (int)(trow * p.k_st * 2) + 16 * ((lane & 15) ^ (row & 15));
     v_voff[h] = (int)(trow * p.v_st * 2) + 16 * ((lane & 15) ^ (4 * lrow));
@@ -335,8 +354,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   // address computations from its table entry.
   const uint32_t lds_base = lds_addr_of(smem);
   auto dma_one = [&](const uint16_t* base, int64_t off, int64_t st, int ts, int lds_off,
-                     const int (&voff)[2], int h, const PagedLoads& pl, int tl) {
-    const int i = is_paged(MODE) ? 2 * wave + h : wave + 8 * h;
+                     const int (&voff)[kLpw], int h, const PagedLoads& pl, int tl) {
+    const int i = is_paged(MODE) ? kLpw * wave + h : wave + kPfWaves * h;
     const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_base + lds_off + 1024 * i);
     if constexpr (is_paged(MODE)) {
       const uint32_t lo = __builtin_amdgcn_readlane(pl.lo, tl);
@@ -348,15 +367,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
       const int rows = ts < 0 ? 0 : sclamp(kv_hi - ts, 0, kPfBc);
       lds_dma16(uniform_u64(reinterpret_cast<uint64_t>(base + off + (int64_t)t0 * st)),
                 __builtin_amdgcn_readfirstlane(rows * (int)st * 2), lds,
-                voff[0] + h * 32 * (int)st * 2);
+                voff[0] + h * 4 * kPfWaves * (int)st * 2);
     }
   };
 
   // First key of each tile of stage j (may be negative or past kv_hi: then nothing is loaded).
+  // (One stream: stage j is V(j) and K(j+1) only; the stream-1 starts are then never used.)
   auto k0_start = [&](int j) { return (j + 1) * kPfStep; };
-  auto k1_start = [&](int j) { return j * kPfStep + kPfBc; };
+  auto k1_start = [&](int j) { return NS == 2 ? j * kPfStep + kPfBc : -1; };
   auto v0_start = [&](int j) { return j * kPfStep; };
-  auto v1_start = [&](int j) { return (j - 1) * kPfStep + kPfBc; };
+  auto v1_start = [&](int j) { return NS == 2 ? (j - 1) * kPfStep + kPfBc : -1; };
 
   // Paged modes work on groups of 16 stages: group m is stages 16m - 1 .. 16m + 14, and lane l
   // of a group register holds stage 16m - 1 + l/4, tile l%4 (K0, K1, V0, V1), so the table reads
@@ -371,7 +391,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
       const int j = 16 * m - 1 + (lane >> 2);
       const int t = lane & 3;
       const int ts = t == 0 ? k0_start(j) : t == 1 ? k1_start(j) : t == 2 ? v0_start(j) : v1_start(j);
-      const int r0 = ts + 8 * wave;
+      const int r0 = ts + 4 * kLpw * wave;
       if (ts >= 0 && ts < kv_hi && r0 < kv_hi)
         return p.block_table[(int64_t)b * p.bt_stride + (r0 >> __builtin_ctz(p.block_size))];
       return -1;
@@ -389,8 +409,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
       const int j = 16 * m - 1 + (lane >> 2);
       const int t = lane & 3;
       const int ts = t == 0 ? k0_start(j) : t == 1 ? k1_start(j) : t == 2 ? v0_start(j) : v1_start(j);
-      const int r0 = ts + 8 * wave;
-      const int n = min(max(kv_hi - r0, 0), 8);
+      const int r0 = ts + 4 * kLpw * wave;
+      const int n = min(max(kv_hi - r0, 0), 4 * kLpw);
       const bool kv = t < 2;
       const int64_t st = kv ? p.k_st : p.v_st;
       const uint16_t* base = kv ? p.k + k_off : p.v + v_off;
@@ -409,15 +429,19 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
   // 4 for V tiles, q = 2*tile + h.  Inside the key loop they are issued one at a time between the
   // MFMAs of the score and PV phases rather than as a burst.  Paged modes: `pl` is the resolved
   // group holding stage j, whose tiles sit in lanes 4 * ((j + 1) % 16) + tile.
+  // With two streams q = 2 * tile + h (tile 0 or 1 of the stage, instruction h of 2); with one
+  // stream the stage holds one K and one V tile and q is the instruction (h of 4).
   auto dma_k = [&](int j, int q, const PagedLoads& pl) {
-    const int o = (j & 1) * kStageBytes + (q >> 1) * kTileBytes;  // j & 1 folds when j's parity is known
-    dma_one(p.k, k_off, p.k_st, (q >> 1) ? k1_start(j) : k0_start(j), o, k_voff, q & 1, pl,
-            4 * ((j + 1) & 15) + (q >> 1));
+    const int t = NS == 2 ? q >> 1 : 0, h = NS == 2 ? q & 1 : q;
+    const int o = (j & 1) * kStageBytes + t * kTileBytes;  // j & 1 folds when j's parity is known
+    dma_one(p.k, k_off, p.k_st, t ? k1_start(j) : k0_start(j), o, k_voff, h, pl,
+            4 * ((j + 1) & 15) + t);
   };
   auto dma_v = [&](int j, int q, const PagedLoads& pl) {
-    const int o = kVRegion + (j & 1) * kStageBytes + (q >> 1) * kTileBytes;
-    dma_one(p.v, v_off, p.v_st, (q >> 1) ? v1_start(j) : v0_start(j), o, v_voff, q & 1, pl,
-            4 * ((j + 1) & 15) + 2 + (q >> 1));
+    const int t = NS == 2 ? q >> 1 : 0, h = NS == 2 ? q & 1 : q;
+    const int o = kVRegion + (j & 1) * kStageBytes + t * kTileBytes;
+    dma_one(p.v, v_off, p.v_st, t ? v1_start(j) : v0_start(j), o, v_voff, h, pl,
+            4 * ((j + 1) & 15) + 2 + t);
   };
   auto load_stage = [&](int j, const PagedLoads& pl) {
     // Prologue stages only (j = -1, 0, constants): a tile that starts before key 0 holds nothing
@@ -426,10 +450,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     // only writes zeros.
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      if (((q >> 1) ? k1_start(j) : k0_start(j)) >= 0) dma_k(j, q, pl);
+      if (((NS == 2 && (q >> 1)) ? k1_start(j) : k0_start(j)) >= 0) dma_k(j, q, pl);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      if (((q >> 1) ? v1_start(j) : v0_start(j)) >= 0) dma_v(j, q, pl);
+      if (((NS == 2 && (q >> 1)) ? v1_start(j) : v0_start(j)) >= 0) dma_v(j, q, pl);
   };
   // Each wave waits for its own loads, then the barrier publishes them to the work-group.
   // The builtin wait tells the compiler its own loads (Q) are done; the assembly one is the real
@@ -698,97 +722,140 @@ __global__ __launch_bounds__(kPfThreads, 2) void fa2_prefill_kernel(const FwdPar
     __syncthreads();
   }
 
-  // The two streams of a row group split the epilogue: each gives the other the half of O it does
-  // not keep (stream 0 keeps d 0..63, stream 1 d 64..127) with its (m, l), merges its own half
-  // and stores it, so the merge, the normalisation and the stores run on all 8 waves instead of
-  // stream 0's 4 (16 packed sequences 43.2 -> 40.5 us, 768 equal 1024-key tiles 66.6 -> 64.9 us).
-  // Exchange area of wave (rg, ks): [32 O values + m + l][lane].
-  float* red = reinterpret_cast<float*>(smem);
-  constexpr int kXVals = 34;
-  {
-    float* dst = red + (rg * kPfStreams + ks) * kXVals * 64 + lane;
-    // d-blocks handed over (whole-vector selects on the wave-uniform stream: a runtime index
-    // into the accumulators would put them in scratch memory)
-    const f32x16 give0 = ks == 0 ? oacc[2] : oacc[0];
-    const f32x16 give1 = ks == 0 ? oacc[3] : oacc[1];
+  if constexpr (NS == 1) {
+    // One stream holds whole rows: normalise all of O and store it.  The rows go through LDS so
+    // that every global store writes whole 256-byte rows: row-major [32 rows][128 d] in this
+    // wave's staging area, 16-byte chunks XOR-swizzled by row % 16.  The loop's last barrier came
+    // after every LDS read and load of the key loop, so the areas may overwrite the K/V stages.
+    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    uint8_t* ot = smem + wave * (32 * 256);
+    // Accumulator r of d-block db is d = 32*db + 8*(r/4) + 4*g + r%4: chunk 4*db + r/4, half g.
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      dst[r * 64] = give0[r];
-      dst[(16 + r) * 64] = give1[r];
-    }
-    dst[32 * 64] = m_run;
-    dst[33 * 64] = l_run;
-  }
-  __syncthreads();
-  const int keep = ks == 0 ? 0 : 2;  // first d-block kept
-  const f32x16 keep0 = ks == 0 ? oacc[0] : oacc[2];
-  const f32x16 keep1 = ks == 0 ? oacc[1] : oacc[3];
-  f32x16 ok[2];
-  {
-    // Rows past T_b keep their lanes for the row-wise stores below (their values are merged,
-    // harmlessly, and never stored).
-    const float* src = red + (rg * kPfStreams + (ks ^ 1)) * kXVals * 64 + lane;
-    // Both streams evaluate the same expression, O = O_0 f_0 + O_1 f_1 with stream 0's state
-    // first, so each half of a row is rounded as if one wave merged the whole row.
-    const float mo = src[32 * 64];
-    const float lo = src[33 * 64];
-    const float M = ks == 0 ? fmaxf(m_run, mo) : fmaxf(mo, m_run);
-    const float M_use = M == -INFINITY ? 0.f : M;
-    const float fs = exp2_fast(m_run - M_use);  // this stream's factor
-    const float fo = exp2_fast(mo - M_use);     // the other's
-    // fma(O_0, f_0, O_1 f_1) spelled out, so that the compiler cannot contract the two streams'
-    // expressions differently.
-    if (ks == 0) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        ok[0][r] = __builtin_fmaf(keep0[r], fs, src[r * 64] * fo);
-        ok[1][r] = __builtin_fmaf(keep1[r], fs, src[(16 + r) * 64] * fo);
-      }
-      l_run = __builtin_fmaf(l_run, fs, lo * fo);
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        ok[0][r] = __builtin_fmaf(src[r * 64], fo, keep0[r] * fs);
-        ok[1][r] = __builtin_fmaf(src[(16 + r) * 64], fo, keep1[r] * fs);
-      }
-      l_run = __builtin_fmaf(lo, fo, l_run * fs);
-    }
-    m_run = M;
-  }
-
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  // Accumulator r of d-block db is d = 32*db + 8*(r/4) + 4*g + r%4: four consecutive d per group.
-  // The wave's half rows go through LDS so that every global store writes whole 128-byte
-  // half rows: row-major [32 rows][64 d] in this wave's staging area (after the exchange areas),
-  // 16-byte chunks XOR-swizzled by row % 8 so that the writes and the reads spread over the banks.
-  // Direct stores from the MFMA layout (16 bytes into each of 32 rows per instruction) measured
-  // 5-7% slower on short tiles when one wave stored whole rows.
-  {
-    uint8_t* ot = reinterpret_cast<uint8_t*>(red + kPfWaves * kXVals * 64) + wave * (32 * 128);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int db = 0; db < 4; ++db) {
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const u32x2 val = {E::pack2(ok[i][rr * 4] * inv, ok[i][rr * 4 + 1] * inv),
-                           E::pack2(ok[i][rr * 4 + 2] * inv, ok[i][rr * 4 + 3] * inv)};
-        *reinterpret_cast<u32x2*>(ot + r32 * 128 + 16 * ((4 * i + rr) ^ (r32 & 7)) + 8 * g) = val;
+        const u32x2 val = {E::pack2(oacc[db][rr * 4] * inv, oacc[db][rr * 4 + 1] * inv),
+                           E::pack2(oacc[db][rr * 4 + 2] * inv, oacc[db][rr * 4 + 3] * inv)};
+        *reinterpret_cast<u32x2*>(ot + r32 * 256 + 16 * ((4 * db + rr) ^ (r32 & 15)) + 8 * g) = val;
       }
     }
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {  // rows 8k .. 8k+7, one 16-byte chunk per lane
-      const int row = 8 * k + (lane >> 3), ch = lane & 7;
-      const u32x4 val = *reinterpret_cast<const u32x4*>(ot + row * 128 + 16 * (ch ^ (row & 7)));
+    for (int k = 0; k < 8; ++k) {  // rows 4k .. 4k+3, one 16-byte chunk per lane
+      const int row = 4 * k + (lane >> 4), ch = lane & 15;
+      const u32x4 val = *reinterpret_cast<const u32x4*>(ot + row * 256 + 16 * (ch ^ (row & 15)));
       if (wq0 + row < T_b)
-        *reinterpret_cast<u32x4*>(p.o + o_off + (int64_t)(wq0 + row) * p.o_st + keep * 32 +
-                                  ch * 8) = val;
+        *reinterpret_cast<u32x4*>(p.o + o_off + (int64_t)(wq0 + row) * p.o_st + ch * 8) = val;
     }
+    if (p.lse && g == 0 && qrow < T_b)
+      p.lse[l_off + (int64_t)qrow * p.l_st] =
+          l_tot > 0.f ? (m_run + __builtin_log2f(l_tot)) * kLn2 : -INFINITY;
+  } else {
+    // The two streams of a row group split the epilogue: each gives the other the half of O it does
+    // not keep (stream 0 keeps d 0..63, stream 1 d 64..127) with its (m, l), merges its own half
+    // and stores it, so the merge, the normalisation and the stores run on all 8 waves instead of
+    // stream 0's 4 (16 packed sequences 43.2 -> 40.5 us, 768 equal 1024-key tiles 66.6 -> 64.9 us).
+    // Exchange area of wave (rg, ks): [32 O values + m + l][lane].
+    float* red = reinterpret_cast<float*>(smem);
+    constexpr int kXVals = 34;
+    {
+      float* dst = red + (rg * NS + ks) * kXVals * 64 + lane;
+      // d-blocks handed over (whole-vector selects on the wave-uniform stream: a runtime index
+      // into the accumulators would put them in scratch memory)
+      const f32x16 give0 = ks == 0 ? oacc[2] : oacc[0];
+      const f32x16 give1 = ks == 0 ? oacc[3] : oacc[1];
+  #pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        dst[r * 64] = give0[r];
+        dst[(16 + r) * 64] = give1[r];
+      }
+      dst[32 * 64] = m_run;
+      dst[33 * 64] = l_run;
+    }
+    __syncthreads();
+    const int keep = ks == 0 ? 0 : 2;  // first d-block kept
+    const f32x16 keep0 = ks == 0 ? oacc[0] : oacc[2];
+    const f32x16 keep1 = ks == 0 ? oacc[1] : oacc[3];
+    f32x16 ok[2];
+    {
+      // Rows past T_b keep their lanes for the row-wise stores below (their values are merged,
+      // harmlessly, and never stored).
+      const float* src = red + (rg * NS + (ks ^ 1)) * kXVals * 64 + lane;
+      // Both streams evaluate the same expression, O = O_0 f_0 + O_1 f_1 with stream 0's state
+      // first, so each half of a row is rounded as if one wave merged the whole row.
+      const float mo = src[32 * 64];
+      const float lo = src[33 * 64];
+      const float M = ks == 0 ? fmaxf(m_run, mo) : fmaxf(mo, m_run);
+      const float M_use = M == -INFINITY ? 0.f : M;
+      const float fs = exp2_fast(m_run - M_use);  // this stream's factor
+      const float fo = exp2_fast(mo - M_use);     // the other's
+      // fma(O_0, f_0, O_1 f_1) spelled out, so that the compiler cannot contract the two streams'
+      // expressions differently.
+      if (ks == 0) {
+  #pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          ok[0][r] = __builtin_fmaf(keep0[r], fs, src[r * 64] * fo);
+          ok[1][r] = __builtin_fmaf(keep1[r], fs, src[(16 + r) * 64] * fo);
+        }
+        l_run = __builtin_fmaf(l_run, fs, lo * fo);
+      } else {
+  #pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          ok[0][r] = __builtin_fmaf(src[r * 64], fo, keep0[r] * fs);
+          ok[1][r] = __builtin_fmaf(src[(16 + r) * 64], fo, keep1[r] * fs);
+        }
+        l_run = __builtin_fmaf(lo, fo, l_run * fs);
+      }
+      m_run = M;
+    }
+
+    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    // Accumulator r of d-block db is d = 32*db + 8*(r/4) + 4*g + r%4: four consecutive d per group.
+    // The wave's half rows go through LDS so that every global store writes whole 128-byte
+    // half rows: row-major [32 rows][64 d] in this wave's staging area (after the exchange areas),
+    // 16-byte chunks XOR-swizzled by row % 8 so that the writes and the reads spread over the banks.
+    // Direct stores from the MFMA layout (16 bytes into each of 32 rows per instruction) measured
+    // 5-7% slower on short tiles when one wave stored whole rows.
+    {
+      uint8_t* ot = reinterpret_cast<uint8_t*>(red + kPfWaves * kXVals * 64) + wave * (32 * 128);
+  #pragma unroll
+      for (int i = 0; i < 2; ++i) {
+  #pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const u32x2 val = {E::pack2(ok[i][rr * 4] * inv, ok[i][rr * 4 + 1] * inv),
+                             E::pack2(ok[i][rr * 4 + 2] * inv, ok[i][rr * 4 + 3] * inv)};
+          *reinterpret_cast<u32x2*>(ot + r32 * 128 + 16 * ((4 * i + rr) ^ (r32 & 7)) + 8 * g) = val;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+  #pragma unroll
+      for (int k = 0; k < 4; ++k) {  // rows 8k .. 8k+7, one 16-byte chunk per lane
+        const int row = 8 * k + (lane >> 3), ch = lane & 7;
+        const u32x4 val = *reinterpret_cast<const u32x4*>(ot + row * 128 + 16 * (ch ^ (row & 7)));
+        if (wq0 + row < T_b)
+          *reinterpret_cast<u32x4*>(p.o + o_off + (int64_t)(wq0 + row) * p.o_st + keep * 32 +
+                                    ch * 8) = val;
+      }
+    }
+    if (ks == 0 && p.lse && g == 0 && qrow < T_b)
+      p.lse[l_off + (int64_t)qrow * p.l_st] =
+          l_tot > 0.f ? (m_run + __builtin_log2f(l_tot)) * kLn2 : -INFINITY;
   }
-  if (ks == 0 && p.lse && g == 0 && qrow < T_b)
-    p.lse[l_off + (int64_t)qrow * p.l_st] =
-        l_tot > 0.f ? (m_run + __builtin_log2f(l_tot)) * kLn2 : -INFINITY;
   probe_mark(p.clock_probe, blockIdx.x, true);
+}
+
+// Key streams per work-group for a launch of `grid` work-groups.  Two streams halve the time of
+// the longest query tile, which is what bounds a launch of about one work-group per CU (one long
+// causal sequence); one stream fits two work-groups per CU, which hides each one's start (item,
+// Q and first stages) and end (stores) behind the other's key loop once there are enough
+// work-groups to fill both slots of every CU.  MI_FA2_PREFILL_STREAMS=1 or 2 forces one shape
+// (read at every launch, so that a test can run both shapes in one process).
+static int prefill_streams(int grid, int n_cus) {
+  const char* e = std::getenv("MI_FA2_PREFILL_STREAMS");
+  if (e != nullptr && (e[0] == '1' || e[0] == '2') && e[1] == 0) return e[0] - '0';
+  return grid >= 2 * n_cus ? 1 : 2;
 }
 
 template <typename E, int MODE>
@@ -801,8 +868,13 @@ static hipError_t launch_prefill_t(const FwdParams& p, int max_seqlen_q, hipStre
   const int X = 1 << p.xcd_log2;
   const int grid = packed ? X * p.group * ((p.B * p.Hkv * n_qt + X - 1) / X)
                           : prefill_grid_size(p.B * p.Hkv, p.group, n_qt, p.xcd_log2);
-  hipLaunchKernelGGL((fa2_prefill_kernel<E, MODE>), dim3(grid), dim3(kPfThreads), 0, stream, p,
-                     n_qt, make_item_map(p.B * p.Hkv, p.group, p.Hkv, p.xcd_log2));
+  const ItemMap map = make_item_map(p.B * p.Hkv, p.group, p.Hkv, p.xcd_log2);
+  if (prefill_streams(grid, p.n_cus) == 1)
+    hipLaunchKernelGGL((fa2_prefill_kernel<E, MODE, 1>), dim3(grid), dim3(PfShape<1>::kThreads), 0,
+                       stream, p, n_qt, map);
+  else
+    hipLaunchKernelGGL((fa2_prefill_kernel<E, MODE, 2>), dim3(grid), dim3(PfShape<2>::kThreads), 0,
+                       stream, p, n_qt, map);
   return hipGetLastError();
 }
 
