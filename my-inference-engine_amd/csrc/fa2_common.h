@@ -90,6 +90,10 @@ struct FP16 {
   }
 };
 
+// Prefill launches of at least this many work-groups (two per CU) use the one-stream
+// work-group shape, which fits two work-groups per CU.
+inline int prefill_one_stream_min_grid(int n_cus) { return 2 * n_cus; }
+
 // Everything a kernel launch needs; passed by value (kernel argument segment).
 struct FwdParams {
   const uint16_t* q;

@@ -855,7 +855,7 @@ __global__ __launch_bounds__(PfShape<NS>::kThreads, 2) void fa2_prefill_kernel(c
 static int prefill_streams(int grid, int n_cus) {
   const char* e = std::getenv("MI_FA2_PREFILL_STREAMS");
   if (e != nullptr && (e[0] == '1' || e[0] == '2') && e[1] == 0) return e[0] - '0';
-  return grid >= 2 * n_cus ? 1 : 2;
+  return grid >= prefill_one_stream_min_grid(n_cus) ? 1 : 2;
 }
 
 template <typename E, int MODE>

@@ -29,7 +29,8 @@ class Plan(ctypes.Structure):
     """mi_fa2_plan: how the launches are sized for a device (its CUs and XCDs)."""
     _fields_ = [("num_cus", ctypes.c_int32), ("num_xcds", ctypes.c_int32),
                 ("xcds_mapped", ctypes.c_int32), ("decode_work_groups_paged", ctypes.c_int32),
-                ("decode_work_groups_dense", ctypes.c_int32)]
+                ("decode_work_groups_dense", ctypes.c_int32),
+                ("prefill_one_stream_min_work_groups", ctypes.c_int32)]
 
 
 # name -> (restype, argtypes); mirrors include/mi_fa2.h
