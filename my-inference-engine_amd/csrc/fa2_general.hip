@@ -419,8 +419,24 @@ __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_split_kernel(FwdPa
   float m_run = -INFINITY, l_run = 0.f;
   const float c = p.scale_log2;
 
+  // A pair's V^T gathers are issued with its K loads, before the score MFMAs, so that a pair
+  // costs one memory round trip instead of two (when a pair's V fits 512 bytes per row).
+  constexpr bool kVPre = DV * (int)sizeof(T) <= 512;
   for (int pr = pr_lo; pr < pr_hi; ++pr) {
     const int kb = 32 * pr;
+    Quad vpre[kVPre ? kVB : 1][2];
+    if constexpr (kVPre) {
+#pragma unroll
+      for (int i = 0; i < kVB; ++i)
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int key = kb + 16 * ch + 4 * g + j;
+            const T* vr = vp + (int64_t)min(key, kv_len - 1) * p.v_st + 16 * i + n;
+            vpre[i][ch][j] = key < kv_len ? G::load1(vr) : 0;
+          }
+    }
     // S^T of the two 16-key chunks: K as the A operand straight from global memory (rows past
     // kv_len read as zero operands, their address clamped to row 0).
     f32x4 st[2];
@@ -473,14 +489,19 @@ __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_split_kernel(FwdPa
 #pragma unroll
     for (int i = 0; i < kVB; ++i) {
       Quad va[2];
+      if constexpr (kVPre) {
+        va[0] = vpre[i][0];
+        va[1] = vpre[i][1];
+      } else {
 #pragma unroll
-      for (int ch = 0; ch < 2; ++ch)
+        for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int key = kb + 16 * ch + 4 * g + j;
-          const T* vr = vp + (int64_t)min(key, kv_len - 1) * p.v_st + 16 * i + n;
-          va[ch][j] = key < kv_len ? G::load1(vr) : 0;
-        }
+          for (int j = 0; j < 4; ++j) {
+            const int key = kb + 16 * ch + 4 * g + j;
+            const T* vr = vp + (int64_t)min(key, kv_len - 1) * p.v_st + 16 * i + n;
+            va[ch][j] = key < kv_len ? G::load1(vr) : 0;
+          }
+      }
       f32x4 acc = oacc[i] * alpha;
       if constexpr (k16) {
         const u32x2 a0 = __builtin_bit_cast(u32x2, va[0]), a1 = __builtin_bit_cast(u32x2, va[1]);
