@@ -9,8 +9,8 @@
 //     by 16 bytes), shared by the 4 waves, two barriers per step; when a step fits 32 KB the next
 //     step's rows are loaded into registers while this one computes.
 //   * fa2_general_split_kernel, for launches that would leave CUs idle (fewer than 64 query rows,
-//     or fewer such work-groups than CUs): the 4 waves share 16 query rows and split their keys,
-//     loading K and V operands straight from global memory, and merge (m, l, O) through LDS.
+//     or fewer such work-groups than CUs): the 4 (or 8) waves share 16 query rows and split their
+//     keys, loading K and V operands straight from global memory, and merge (m, l, O) through LDS.
 //   * S^T = K Q^T leaves lane l with query column l%16 and keys 4*(l/16) + r of a 16-key chunk,
 //     which is exactly the B-operand layout of O^T += V^T P^T: P never leaves registers.  16-bit
 //     types run both products on v_mfma_f32_16x16x32 (8 consecutive d per lane for the scores,
@@ -364,12 +364,14 @@ __global__ __launch_bounds__(64 * kGenWaves) void fa2_general_kernel(FwdParams p
 
 // Key-split variant for launches that would leave the chip idle: fewer query rows than a
 // work-group of fa2_general_kernel holds (decode-shaped calls), or fewer of those work-groups
-// than CUs (a short sequence with few heads).  A work-group = 4 waves on the SAME 16 query rows;
-// wave w walks the w-th quarter of the 32-key pairs those rows see, loading its K and V operands
-// straight from global memory (no LDS, no barrier in the loop), and the 4 waves' (m, l, O) are
-// merged through LDS at the end, each wave finishing every 4th d-block.
-template <class E, int D, int DV>
-__global__ __launch_bounds__(64 * kGenWaves) void fa2_general_split_kernel(FwdParams p) {
+// than CUs (a short sequence with few heads).  A work-group = W waves on the SAME 16 query rows;
+// wave w walks the w-th W-th of the 32-key pairs those rows see, loading its K and V operands
+// straight from global memory (no LDS, no barrier in the loop), and the W waves' (m, l, O) are
+// merged through LDS at the end, each wave finishing every W-th d-block.  W = 4, or 8 (twice the
+// key split) when the grid leaves a whole CU to each work-group (d_v <= 128).
+template <class E, int D, int DV, int W>
+__global__ __launch_bounds__(64 * W) void fa2_general_split_kernel(FwdParams p) {
+  constexpr int kGenWaves = W;
   using G = Gen<E>;
   using T = typename G::T;
   using Quad = typename G::Quad;
@@ -565,8 +567,17 @@ hipError_t launch_general_t(const FwdParams& p, hipStream_t stream) {
   // the chain).
   if (p.T < rows_per_wg || tiles < p.n_cus) {
     const dim3 grid((p.T + kGenRows - 1) / kGenRows, p.Hq, p.B);
-    hipLaunchKernelGGL((fa2_general_split_kernel<E, D, DV>), grid, dim3(64 * kGenWaves), 0,
-                       stream, p);
+    // Eight waves when every work-group can have a CU of its own (two waves per SIMD): an fp32
+    // call of 16 rows x 1 query x 2,048 keys took 114 -> 84 us; with more work-groups than CUs the
+    // four-wave shape, two work-groups per CU, is faster (1 x 12 x 512 fp32: 35.7 against 37.3 us).
+    if constexpr (DV <= 128) {
+      if ((int64_t)grid.x * grid.y * grid.z <= p.n_cus) {
+        hipLaunchKernelGGL((fa2_general_split_kernel<E, D, DV, 8>), grid, dim3(64 * 8), 0, stream,
+                           p);
+        return hipGetLastError();
+      }
+    }
+    hipLaunchKernelGGL((fa2_general_split_kernel<E, D, DV, 4>), grid, dim3(64 * 4), 0, stream, p);
     return hipGetLastError();
   }
   const dim3 grid((p.T + rows_per_wg - 1) / rows_per_wg, p.Hq, p.B);
