@@ -660,7 +660,9 @@ __global__ __launch_bounds__(PfShape<NS>::kThreads, 2) void fa2_prefill_kernel(c
       step(j + 1, Parity<1>{});
     }
     if (j < n_steps) step(j, Parity<0>{});
-    __syncthreads();  // pairs with stream 1's barrier after its last PV
+    // Two streams: pairs with stream 1's barrier after its last PV.  One stream: the loop's last
+    // barrier already follows every LDS read; this one is kept so both shapes share the code.
+    __syncthreads();
   } else {
     u32x4 pbv[4];  // P of the previous tile, carried across the barrier
     __syncthreads();
