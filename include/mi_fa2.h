@@ -74,9 +74,10 @@ MI_FA2_API const char* mi_fa2_last_error(void);
  *   xcds_mapped: XCDs the prefill grid deals work-groups over (num_xcds if a power of two, else 1)
  *   decode_work_groups_*: split-decode work-groups per launch (3 or 2 per CU; MI_FA2_DECODE_WGS
  *   overrides both), capped at run time by the launch's 128-key chunk count.
- *   prefill_one_stream_min_work_groups: prefill launches of at least this many work-groups (two
- *   per CU) take the one-stream work-group shape (4 waves, two work-groups per CU), smaller ones
- *   the two-stream shape (8 waves, one per CU); MI_FA2_PREFILL_STREAMS=1 or 2 forces one shape.
+ *   prefill_one_stream_min_work_groups, prefill_one_stream_max_keys: prefill launches of at
+ *   least that many work-groups (two per CU) whose query tiles see at most that many keys take
+ *   the one-stream work-group shape (4 waves, two work-groups per CU), the others the two-stream
+ *   shape (8 waves, one per CU); MI_FA2_PREFILL_STREAMS=1 or 2 forces one shape.
  */
 typedef struct mi_fa2_plan {
   int32_t num_cus;
@@ -85,6 +86,7 @@ typedef struct mi_fa2_plan {
   int32_t decode_work_groups_paged;
   int32_t decode_work_groups_dense;
   int32_t prefill_one_stream_min_work_groups;
+  int32_t prefill_one_stream_max_keys;
 } mi_fa2_plan;
 MI_FA2_API int mi_fa2_launch_plan(int32_t num_cus, int32_t num_xcds, mi_fa2_plan* out);
 

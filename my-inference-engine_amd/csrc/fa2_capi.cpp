@@ -375,6 +375,7 @@ int mi_fa2_launch_plan(int32_t num_cus, int32_t num_xcds, mi_fa2_plan* out) {
   out->decode_work_groups_paged = pl.decode_wgs_paged;
   out->decode_work_groups_dense = pl.decode_wgs_dense;
   out->prefill_one_stream_min_work_groups = mi_fa2::prefill_one_stream_min_grid(pl.cus);
+  out->prefill_one_stream_max_keys = mi_fa2::kPrefillOneStreamMaxKeys;
   return ok();
 }
 

@@ -848,16 +848,20 @@ __global__ __launch_bounds__(PfShape<NS>::kThreads, 2) void fa2_prefill_kernel(c
   probe_mark(p.clock_probe, blockIdx.x, true);
 }
 
-// Key streams per work-group for a launch of `grid` work-groups.  Two streams halve the time of
-// the longest query tile, which is what bounds a launch of about one work-group per CU (one long
-// causal sequence); one stream fits two work-groups per CU, which hides each one's start (item,
-// Q and first stages) and end (stores) behind the other's key loop once there are enough
-// work-groups to fill both slots of every CU.  MI_FA2_PREFILL_STREAMS=1 or 2 forces one shape
-// (read at every launch, so that a test can run both shapes in one process).
-static int prefill_streams(int grid, int n_cus) {
+// Key streams per work-group for a launch of `grid` work-groups whose query tiles see at most
+// `max_keys` keys.  Two streams halve the time of the longest query tile, which is what bounds a
+// launch of about one work-group per CU (one long causal sequence); one stream fits two
+// work-groups per CU, which hides each one's start (item, Q and first stages) and end (stores)
+// behind the other's key loop once there are enough work-groups to fill both slots of every CU
+// and the tiles are short enough for those to matter.  Measured (us per launch, two streams / one
+// stream): 2 x 4096 causal 111.1 / 107.5, 3 x 4096 165.8 / 159.3, 16 packed rows of up to 1024
+// 40.8 / 30.6; 1 x 6144 causal 122.8 / 134.4, 1 x 16384 causal 726 / 741.  MI_FA2_PREFILL_STREAMS
+// = 1 or 2 forces one shape (read at every launch, so that a test can run both in one process).
+static int prefill_streams(int grid, int n_cus, int max_keys) {
   const char* e = std::getenv("MI_FA2_PREFILL_STREAMS");
   if (e != nullptr && (e[0] == '1' || e[0] == '2') && e[1] == 0) return e[0] - '0';
-  return grid >= prefill_one_stream_min_grid(n_cus) ? 1 : 2;
+  return grid >= prefill_one_stream_min_grid(n_cus) && max_keys <= kPrefillOneStreamMaxKeys ? 1
+                                                                                            : 2;
 }
 
 template <typename E, int MODE>
@@ -871,7 +875,10 @@ static hipError_t launch_prefill_t(const FwdParams& p, int max_seqlen_q, hipStre
   const int grid = packed ? X * p.group * ((p.B * p.Hkv * n_qt + X - 1) / X)
                           : prefill_grid_size(p.B * p.Hkv, p.group, n_qt, p.xcd_log2);
   const ItemMap map = make_item_map(p.B * p.Hkv, p.group, p.Hkv, p.xcd_log2);
-  if (prefill_streams(grid, p.n_cus) == 1)
+  // Keys a query tile sees at most: the padded key count, or for packed rows (no key bound
+  // given) the longest row's query count, which bounds them for causal self-attention batches.
+  const int max_keys = p.S > 0 ? p.S : max_seqlen_q;
+  if (prefill_streams(grid, p.n_cus, max_keys) == 1)
     hipLaunchKernelGGL((fa2_prefill_kernel<E, MODE, 1>), dim3(grid), dim3(PfShape<1>::kThreads), 0,
                        stream, p, n_qt, map);
   else

@@ -30,7 +30,8 @@ class Plan(ctypes.Structure):
     _fields_ = [("num_cus", ctypes.c_int32), ("num_xcds", ctypes.c_int32),
                 ("xcds_mapped", ctypes.c_int32), ("decode_work_groups_paged", ctypes.c_int32),
                 ("decode_work_groups_dense", ctypes.c_int32),
-                ("prefill_one_stream_min_work_groups", ctypes.c_int32)]
+                ("prefill_one_stream_min_work_groups", ctypes.c_int32),
+                ("prefill_one_stream_max_keys", ctypes.c_int32)]
 
 
 # name -> (restype, argtypes); mirrors include/mi_fa2.h

@@ -55,7 +55,8 @@ def test_launch_plan_follows_the_device_topology(cus, xcds, mapped, paged, dense
     pl = _lib.launch_plan(cus, xcds)
     assert pl == {"num_cus": cus, "num_xcds": xcds, "xcds_mapped": mapped,
                   "decode_work_groups_paged": paged, "decode_work_groups_dense": dense,
-                  "prefill_one_stream_min_work_groups": 2 * cus}
+                  "prefill_one_stream_min_work_groups": 2 * cus,
+                  "prefill_one_stream_max_keys": 4096}
 
 
 def test_launch_plan_and_clock_probe_reject_bad_arguments():
