@@ -428,7 +428,7 @@ def main():
     global RAMP_MS
     RAMP_MS = args.ramp_ms
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build's hot path runs on a single MI355X "
+        print(f"bench.py measures one GPU: the attention path runs on a single MI355X "
               f"(--gpus {args.gpus} is not supported)", file=sys.stderr)
         sys.exit(2)
 

@@ -1,7 +1,7 @@
 """CPU oracle of the attention hot path.  TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package, and
-only as the checker (or the timed CPU baseline), never as part of the product path.
+only to check results (or as the timed CPU baseline), never as part of the product path.
 
 Contents (each function cites the reference lines it restates; nothing is imported from the
 reference):
